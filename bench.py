@@ -1,0 +1,295 @@
+"""Decision-prefill benchmark on one MI355X.
+
+Workload (one "step"): the full 9B-shaped decision forward — 42 layers, H 3584,
+16/8 GQA heads x 256, MLP 14336, vocab 256000, sliding 4096 / global
+alternation, softcap 50 (final 30), random-init bf16 — over a batch of 16
+requests with ragged prompt lengths drawn log-uniform in [256, 16384] and
+uniform-random token ids; 8 questions per request with 2-8 options each, read
+at distinct positions in the last min(L, 512) tokens. Inputs are resident in
+HBM before the timed region.
+
+Prints one JSON line: prefill tokens/s (value), decisions/s, TFLOP/s, the
+attention kernel's TFLOP/s and MFMA fraction, the dominant kernel's roofline,
+and the CPU oracle baseline timed on a bounded sample on this host.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from collections import defaultdict
+from dataclasses import replace
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+PEAK_BF16 = 2.5e15      # MI355X dense bf16 MFMA, FLOP/s
+PEAK_HBM = 8.0e12       # bytes/s
+BATCH, QUESTIONS = 16, 8
+LEN_LO, LEN_HI = 256, 16384
+
+
+def synthetic_batch(vocab: int, seed: int = 0):
+    r = np.random.Generator(np.random.PCG64(seed))
+    lengths = np.rint(np.exp(r.uniform(math.log(LEN_LO), math.log(LEN_HI), BATCH))).astype(int).tolist()
+    ids = [r.integers(0, vocab, n).tolist() for n in lengths]
+    options = []
+    for n in lengths:
+        tail = min(n, 512)
+        counts = r.integers(2, 9, QUESTIONS)
+        pos = r.choice(np.arange(n - tail, n), size=int(counts.sum()), replace=False)
+        req, used = [], 0
+        for c in counts:
+            req.append([(int(p), int(r.integers(0, vocab))) for p in pos[used:used + c]])
+            used += int(c)
+        options.append(req)
+    return lengths, ids, options
+
+
+class KernelTimer:
+    """HIP events around every kernel launch, on the stream the launch uses (torch's current
+    stream): per-category launch counts and average durations over the timed steps."""
+
+    def __init__(self, K, config) -> None:
+        import torch
+
+        self.torch = torch
+        self.K = K
+        self.cfg = config
+        self.events: dict[str, list] = defaultdict(list)
+        self.enabled = False
+        self._orig = {}
+        qkv_rows = config.qkv_width
+
+        def wrap(fname, label_fn):
+            orig = getattr(K, fname)
+            self._orig[fname] = orig
+
+            def inner(*args, **kwargs):
+                if not self.enabled:
+                    return orig(*args, **kwargs)
+                a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                a.record()
+                out = orig(*args, **kwargs)
+                b.record()
+                self.events[label_fn(args, kwargs)].append((a, b))
+                return out
+
+            setattr(K, fname, inner)
+
+        def linear_label(args, kwargs):
+            w = args[1]
+            if w.shape[0] == qkv_rows:
+                return "qkv_proj"
+            if w.shape[1] == config.intermediate:
+                return "down_proj"
+            return "o_proj"
+
+        wrap("linear", linear_label)
+        wrap("gated_linear", lambda a, k: "gate_up_proj")
+        wrap("attention_vt", lambda a, k: "attention_sliding" if k.get("window", 0) else "attention_global")
+        wrap("add_rmsnorm", lambda a, k: "add_rmsnorm")
+        wrap("rope", lambda a, k: "rope")
+        wrap("transpose_v", lambda a, k: "transpose_v")
+        wrap("embed", lambda a, k: "embed")
+        wrap("readout", lambda a, k: "readout")
+
+    def restore(self) -> None:
+        for k, v in self._orig.items():
+            setattr(self.K, k, v)
+
+    def summary(self) -> dict[str, dict[str, float]]:
+        out = {}
+        for name, evs in self.events.items():
+            ms = [a.elapsed_time(b) for a, b in evs]
+            out[name] = {"launches": len(ms), "avg_ms": float(np.mean(ms)), "total_ms": float(np.sum(ms))}
+        return out
+
+
+def algorithmic_work(cfg, lengths: list[int]) -> dict[str, float]:
+    """Algorithmic FLOPs of one launch (one layer) of each GEMM / attention category."""
+    t = sum(lengths)
+    h, d, hq = cfg.hidden, cfg.head_dim, cfg.heads
+    # attention_flops of a one-layer config: layer 0 is a sliding layer; window 0 makes it global
+    one = replace(cfg, layers=1)
+    return {
+        "qkv_proj": 2.0 * t * h * cfg.qkv_width,
+        "o_proj": 2.0 * t * hq * d * h,
+        "gate_up_proj": 2.0 * t * h * 2 * cfg.intermediate,
+        "down_proj": 2.0 * t * cfg.intermediate * h,
+        "attention_sliding": float(one.attention_flops(lengths)),
+        "attention_global": float(replace(one, window=0).attention_flops(lengths)),
+    }
+
+
+def cpu_baseline(cfg, seconds_budget: float = 20.0) -> dict:
+    """The oracle (numpy fp32 restatement of the path, bf16 rounding points) on a bounded sample:
+    one request of 512 tokens through one sliding and one global layer of the 9B shape plus the
+    readout; the measured FLOP rate is extrapolated to the full batch by its FLOP count."""
+    from oracle import model as om
+
+    try:
+        from threadpoolctl import threadpool_info
+        threads = max((i.get("num_threads", 1) for i in threadpool_info()), default=1)
+    except Exception:  # pragma: no cover
+        threads = len(os.sched_getaffinity(0))
+    r = np.random.Generator(np.random.PCG64(1))
+    n, layers = 512, 2
+    shape = om.Shape(hidden=cfg.hidden, heads=cfg.heads, kv_heads=cfg.kv_heads, head_dim=cfg.head_dim,
+                     intermediate=cfg.intermediate, vocab=cfg.vocab, layers=layers, window=cfg.window,
+                     query_scale=cfg.query_scale)
+    from oracle.numerics import bf16
+
+    def mat(*s):
+        return bf16((r.standard_normal(s, dtype=np.float32) * np.float32(0.02)))
+
+    vocab_rows = 4096  # the sample only gathers from these rows
+    w = {"embed": mat(vocab_rows, cfg.hidden), "final_norm": mat(cfg.hidden)}
+    for i in range(layers):
+        p = f"layers.{i}."
+        w.update({p + "input_norm": mat(cfg.hidden), p + "q": mat(cfg.heads * cfg.head_dim, cfg.hidden),
+                  p + "k": mat(cfg.kv_heads * cfg.head_dim, cfg.hidden),
+                  p + "v": mat(cfg.kv_heads * cfg.head_dim, cfg.hidden), p + "o": mat(cfg.hidden, cfg.heads * cfg.head_dim),
+                  p + "post_attn_norm": mat(cfg.hidden), p + "pre_ffn_norm": mat(cfg.hidden),
+                  p + "gate": mat(cfg.intermediate, cfg.hidden), p + "up": mat(cfg.intermediate, cfg.hidden),
+                  p + "down": mat(cfg.hidden, cfg.intermediate), p + "post_ffn_norm": mat(cfg.hidden)})
+    ids = r.integers(0, vocab_rows, n)
+    pos = np.arange(n)
+    opt_pos = np.arange(n - 40, n)
+    opt_lab = r.integers(0, vocab_rows, 40)
+    q_off = list(range(0, 41, 5))
+    times = []
+    t_end = time.perf_counter() + seconds_budget
+    while len(times) < 5 and (not times or time.perf_counter() + times[-1] < t_end):
+        t0 = time.perf_counter()
+        x = om.forward(w, shape, ids, [0], [n], pos)
+        om.readout(x, w["final_norm"], w["embed"], opt_pos, opt_lab, q_off, eps=cfg.eps, cap=cfg.final_softcap)
+        times.append(time.perf_counter() - t0)
+    sample_flops = n * replace(cfg, layers=layers).linear_flops_per_token() + replace(cfg, layers=layers).attention_flops([n])
+    t = float(np.median(times))
+    return {"flop_rate": sample_flops / t, "seconds": t, "runs": len(times), "threads": threads,
+            "sample": f"1 request x {n} tokens, 1 sliding + 1 global 9B-shaped layer + readout, numpy fp32 oracle, "
+                      f"median of {len(times)}; tokens/s extrapolated by FLOP count to the 42-layer batch"}
+
+
+def main() -> None:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=3)
+    ap.add_argument("--warmup", type=int, default=1)
+    ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one MI355X: the decision path runs on a single GPU (data parallel over requests "
+              "needs no exchange); run it with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    from deciax_amd import gemma
+    from deciax_amd import kernels as K
+
+    cfg = gemma.CONFIGS["gemma2-9b"]
+    t0 = time.time()
+    weights = gemma.random_weights(cfg, seed=args.seed)
+    torch.cuda.synchronize()
+    print(f"# weights {weights.nbytes() / 1e9:.1f} GB in {time.time() - t0:.1f}s", file=sys.stderr, flush=True)
+    lengths, ids, options = synthetic_batch(cfg.vocab, seed=args.seed)
+    batch = gemma.pack_batch(ids, options)
+    ws = gemma.Workspace(cfg, batch.rows, batch.vt_ld, weights.device)
+    tokens = batch.rows
+    print(f"# batch {len(lengths)} requests, {tokens} tokens, lengths {lengths}", file=sys.stderr, flush=True)
+
+    timer = KernelTimer(K, cfg)
+    for i in range(args.warmup):
+        gemma.forward(weights, batch, ws)
+        torch.cuda.synchronize()
+        print(f"# warmup {i + 1}/{args.warmup} done", file=sys.stderr, flush=True)
+
+    timer.enabled = True
+    torch.cuda.synchronize()
+    start = time.perf_counter()
+    for i in range(args.steps):
+        logits, probs = gemma.forward(weights, batch, ws)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - start
+    timer.enabled = False
+    timer.restore()
+    assert torch.isfinite(probs).all().item(), "non-finite probabilities"
+    ms = elapsed / args.steps * 1e3
+    print(f"# {args.steps} steps, {ms:.1f} ms/step", file=sys.stderr, flush=True)
+
+    kern = timer.summary()
+    work = algorithmic_work(cfg, lengths)
+    total_flops = tokens * cfg.linear_flops_per_token() + cfg.attention_flops(lengths)
+    per_kernel = {}
+    for name, s in sorted(kern.items(), key=lambda kv: -kv[1]["total_ms"]):
+        entry = dict(s)
+        entry["share"] = s["total_ms"] / (ms * args.steps)
+        if name in work and s["launches"]:
+            entry["tflops"] = work[name] / (s["avg_ms"] * 1e-3) / 1e12
+            entry["frac_bf16_peak"] = entry["tflops"] * 1e12 / PEAK_BF16
+        per_kernel[name] = entry
+    dominant = max(kern, key=lambda k: kern[k]["total_ms"])
+    dom = per_kernel[dominant]
+    roofline = {
+        "kernel": dominant,
+        "bound": "mfma",
+        "achieved": round(dom.get("tflops", 0.0), 2),
+        "peak": PEAK_BF16 / 1e12,
+        "unit": "TFLOP/s",
+        "frac": round(dom.get("frac_bf16_peak", 0.0), 4),
+        "traffic": None,
+        "algorithmic_flop_per_launch": work.get(dominant, 0.0),
+    }
+    attn_ms = sum(kern[k]["total_ms"] for k in kern if k.startswith("attention")) / args.steps
+    attn_flops = cfg.attention_flops(lengths)
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        print("# cpu baseline (oracle sample)", file=sys.stderr, flush=True)
+        cb = cpu_baseline(cfg)
+        cpu = {"value": round(cb["flop_rate"] / (total_flops / tokens), 2), "unit": "tokens/s",
+               "cores": cb["threads"], "kind": "port", "sample": cb["sample"],
+               "sample_seconds": round(cb["seconds"], 3), "extrapolated": True}
+
+    result = {
+        "metric": "prefill tokens/s (9B-shaped decision forward, 1 GPU)",
+        "value": round(tokens / (ms * 1e-3), 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 2),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (random-init weights, uniform-random token ids)",
+        "config": {"workload": "gemma2-9b-shaped decision forward, 42 layers, batch 16, lengths log-uniform "
+                               "[256, 16384] (seed 0), 8 questions x 2-8 options",
+                   "tokens_per_step": tokens, "requests": len(lengths), "lengths": lengths},
+        "decisions_per_s": round(len(lengths) / (ms * 1e-3), 3),
+        "questions_per_s": round(len(lengths) * QUESTIONS / (ms * 1e-3), 2),
+        "tflops": round(total_flops / (ms * 1e-3) / 1e12, 2),
+        "frac_bf16_peak": round(total_flops / (ms * 1e-3) / PEAK_BF16, 4),
+        "attention": {"tflops": round(attn_flops / (attn_ms * 1e-3) / 1e12, 2),
+                      "frac_bf16_peak": round(attn_flops / (attn_ms * 1e-3) / PEAK_BF16, 4),
+                      "ms_per_step": round(attn_ms, 2)},
+        "kernels": per_kernel,
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(result))
+
+
+if __name__ == "__main__":
+    main()

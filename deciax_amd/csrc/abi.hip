@@ -1,0 +1,337 @@
+// extern "C" entry points declared in include/deciax_hip.h: argument
+// validation, then dispatch to the kernel launchers. Nothing here allocates
+// or synchronises.
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "common.h"
+#include "kernels.h"
+
+namespace {
+
+thread_local char g_err[512];
+
+int fail(int code, const char *fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int check_launch(hipError_t e, const char *what) {
+  if (e != hipSuccess) return fail(DX_ERR_RUNTIME, "%s: %s", what, hipGetErrorString(e));
+  g_err[0] = 0;
+  return DX_OK;
+}
+
+bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+hipStream_t as_stream(void *s) { return reinterpret_cast<hipStream_t>(s); }
+
+#define REQUIRE(cond, ...)                                   \
+  do {                                                       \
+    if (!(cond)) return fail(DX_ERR_INVALID, __VA_ARGS__);   \
+  } while (0)
+#define SUPPORTED(cond, ...)                                    \
+  do {                                                          \
+    if (!(cond)) return fail(DX_ERR_UNSUPPORTED, __VA_ARGS__);  \
+  } while (0)
+
+int64_t align_up(int64_t v, int64_t a) { return (v + a - 1) / a * a; }
+
+int validate_attn(const void *q, const void *k, const void *v, const void *out, const int32_t *seq_start,
+                  const int32_t *seq_len, int32_t num_seqs, int32_t max_seq_len, int32_t hq, int32_t hkv,
+                  int32_t d, int64_t qs, int64_t ks, int64_t os, float scale, float softcap, int32_t window,
+                  int32_t dtype) {
+  REQUIRE(q && k && v && out && seq_start && seq_len, "attention: null pointer argument");
+  REQUIRE(num_seqs >= 0 && max_seq_len >= 0, "attention: negative sequence count or length");
+  REQUIRE(hq > 0 && hkv > 0 && hq % hkv == 0, "attention: num_q_heads %d must be a positive multiple of num_kv_heads %d",
+          hq, hkv);
+  REQUIRE(window >= 0, "attention: window must be >= 0, got %d", window);
+  REQUIRE(softcap >= 0.f && scale > 0.f, "attention: need scale > 0 and softcap >= 0");
+  REQUIRE(dtype == DX_BF16 || dtype == DX_F32, "attention: unknown dtype %d", dtype);
+  SUPPORTED(d == 64 || d == 128 || d == 256, "attention: head_dim %d not in {64, 128, 256}", d);
+  if (dtype == DX_BF16) SUPPORTED(hq / hkv == 1 || hq / hkv == 2 || hq / hkv == 4,
+                                  "attention: bf16 GQA group %d not in {1, 2, 4}", hq / hkv);
+  const int64_t vec = dtype == DX_BF16 ? 8 : 4;
+  REQUIRE(qs % vec == 0 && ks % vec == 0 && os % vec == 0, "attention: row strides must be multiples of %ld elements",
+          (long)vec);
+  REQUIRE(qs >= (int64_t)hq * d && ks >= (int64_t)hkv * d && os >= (int64_t)hq * d,
+          "attention: row stride smaller than heads * head_dim");
+  REQUIRE(aligned16(q) && aligned16(k) && aligned16(v) && aligned16(out), "attention: pointers must be 16-byte aligned");
+  return DX_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char *dx_version(void) { return "deciax-mi355x 0.1.0 gfx950"; }
+
+const char *dx_last_error(void) { return g_err; }
+
+int dx_device_arch(int device, char *buf, int buf_len) {
+  if (!buf || buf_len <= 0) return fail(DX_ERR_INVALID, "dx_device_arch: empty buffer");
+  hipDeviceProp_t prop;
+  hipError_t e = hipGetDeviceProperties(&prop, device);
+  if (e != hipSuccess) return fail(DX_ERR_RUNTIME, "hipGetDeviceProperties: %s", hipGetErrorString(e));
+  int n = 0;
+  while (prop.gcnArchName[n] && prop.gcnArchName[n] != ':' && n < buf_len - 1) {
+    buf[n] = prop.gcnArchName[n];
+    ++n;
+  }
+  buf[n] = 0;
+  return DX_OK;
+}
+
+int64_t dx_attn_prefill_workspace(int32_t num_seqs, int32_t max_seq_len, int32_t num_kv_heads, int32_t head_dim,
+                                  int32_t dtype) {
+  if (dtype != DX_BF16 || num_seqs <= 0 || max_seq_len <= 0) return 0;
+  // V^T with one 64-aligned column block per sequence.
+  return align_up(max_seq_len, 64) * num_seqs * num_kv_heads * head_dim * 2;
+}
+
+int dx_attn_prefill(const void *q, const void *k, const void *v, void *out, const int32_t *seq_start,
+                    const int32_t *seq_len, int32_t num_seqs, int32_t max_seq_len, int32_t num_q_heads,
+                    int32_t num_kv_heads, int32_t head_dim, int64_t q_row_stride, int64_t k_row_stride,
+                    int64_t v_row_stride, int64_t out_row_stride, float scale, float softcap, int32_t window,
+                    int32_t causal, int32_t dtype, void *workspace, int64_t workspace_bytes, void *stream) {
+  int st = validate_attn(q, k, v, out, seq_start, seq_len, num_seqs, max_seq_len, num_q_heads, num_kv_heads,
+                         head_dim, q_row_stride, k_row_stride, out_row_stride, scale, softcap, window, dtype);
+  if (st) return st;
+  const int64_t vec = dtype == DX_BF16 ? 8 : 4;
+  REQUIRE(v_row_stride % vec == 0 && v_row_stride >= (int64_t)num_kv_heads * head_dim,
+          "attention: bad v row stride %ld", (long)v_row_stride);
+  if (num_seqs == 0 || max_seq_len == 0) return DX_OK;
+  AttnArgs a{q, k, v, out, seq_start, seq_len, nullptr, num_seqs, max_seq_len, num_q_heads, num_kv_heads, head_dim,
+             q_row_stride, k_row_stride, v_row_stride, out_row_stride, 0, scale, softcap, window, causal ? 1 : 0};
+  if (dtype == DX_F32) return check_launch(dx_attn_f32(a, as_stream(stream)), "attention fp32 launch");
+
+  const int64_t seq_stride = align_up(max_seq_len, 64);
+  const int64_t vt_ld = seq_stride * num_seqs;
+  const int64_t need = dx_attn_prefill_workspace(num_seqs, max_seq_len, num_kv_heads, head_dim, DX_BF16);
+  REQUIRE(workspace && aligned16(workspace), "attention: bf16 needs a 16-byte aligned workspace");
+  REQUIRE(workspace_bytes >= need, "attention: workspace of %ld bytes, need %ld", (long)workspace_bytes, (long)need);
+  uint16_t *vt = static_cast<uint16_t *>(workspace);
+  hipError_t e = dx_transpose_v_launch(static_cast<const uint16_t *>(v), vt, seq_start, seq_len, nullptr, seq_stride,
+                                       num_seqs, max_seq_len, num_kv_heads, head_dim, v_row_stride, vt_ld,
+                                       as_stream(stream));
+  if (e != hipSuccess) return check_launch(e, "transpose_v launch");
+  a.v = vt;
+  a.v_stride = vt_ld;
+  a.vt_seq_stride = seq_stride;
+  return check_launch(dx_attn_bf16(a, as_stream(stream)), "attention bf16 launch");
+}
+
+int dx_attn_prefill_vt(const void *q, const void *k, const void *vt, void *out, const int32_t *seq_start,
+                       const int32_t *seq_len, const int32_t *vt_start, int32_t num_seqs, int32_t max_seq_len,
+                       int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim, int64_t q_row_stride,
+                       int64_t k_row_stride, int64_t vt_ld, int64_t out_row_stride, float scale, float softcap,
+                       int32_t window, int32_t causal, void *stream) {
+  int st = validate_attn(q, k, vt, out, seq_start, seq_len, num_seqs, max_seq_len, num_q_heads, num_kv_heads,
+                         head_dim, q_row_stride, k_row_stride, out_row_stride, scale, softcap, window, DX_BF16);
+  if (st) return st;
+  REQUIRE(vt_start, "attention: vt_start must not be null");
+  REQUIRE(vt_ld % 8 == 0 && vt_ld > 0, "attention: vt_ld must be a positive multiple of 8");
+  if (num_seqs == 0 || max_seq_len == 0) return DX_OK;
+  AttnArgs a{q, k, vt, out, seq_start, seq_len, vt_start, num_seqs, max_seq_len, num_q_heads, num_kv_heads,
+             head_dim, q_row_stride, k_row_stride, vt_ld, out_row_stride, 0, scale, softcap, window, causal ? 1 : 0};
+  return check_launch(dx_attn_bf16(a, as_stream(stream)), "attention bf16 launch");
+}
+
+int dx_transpose_v(const void *v, void *vt, const int32_t *seq_start, const int32_t *seq_len,
+                   const int32_t *vt_start, int32_t num_seqs, int32_t max_seq_len, int32_t num_kv_heads,
+                   int32_t head_dim, int64_t v_row_stride, int64_t vt_ld, void *stream) {
+  REQUIRE(v && vt && seq_start && seq_len && vt_start, "transpose_v: null pointer argument");
+  REQUIRE(aligned16(v) && aligned16(vt), "transpose_v: pointers must be 16-byte aligned");
+  SUPPORTED(head_dim % 64 == 0, "transpose_v: head_dim %d not a multiple of 64", head_dim);
+  REQUIRE(v_row_stride % 8 == 0 && vt_ld % 8 == 0, "transpose_v: strides must be multiples of 8");
+  REQUIRE(num_seqs >= 0 && max_seq_len >= 0 && num_kv_heads > 0, "transpose_v: bad sizes");
+  if (num_seqs == 0 || max_seq_len == 0) return DX_OK;
+  return check_launch(dx_transpose_v_launch(static_cast<const uint16_t *>(v), static_cast<uint16_t *>(vt), seq_start,
+                                            seq_len, vt_start, 0, num_seqs, max_seq_len, num_kv_heads, head_dim,
+                                            v_row_stride, vt_ld, as_stream(stream)),
+                      "transpose_v launch");
+}
+
+int dx_linear(const void *x, const void *w, void *y, int64_t m, int64_t n, int64_t k, int64_t ldx, int64_t ldw,
+              int64_t ldy, int32_t out_dtype, void *stream) {
+  REQUIRE(x && w && y, "linear: null pointer argument");
+  REQUIRE(m >= 0 && n > 0 && k > 0, "linear: bad sizes m=%ld n=%ld k=%ld", (long)m, (long)n, (long)k);
+  SUPPORTED(n % 256 == 0, "linear: n=%ld must be a multiple of 256", (long)n);
+  SUPPORTED(k % 64 == 0, "linear: k=%ld must be a multiple of 64", (long)k);
+  REQUIRE(ldx >= k && ldw >= k && ldy >= n && ldx % 8 == 0 && ldw % 8 == 0 && ldy % 8 == 0,
+          "linear: leading dimensions must cover the row and be multiples of 8");
+  REQUIRE(aligned16(x) && aligned16(w) && aligned16(y), "linear: pointers must be 16-byte aligned");
+  REQUIRE(out_dtype == DX_BF16 || out_dtype == DX_F32, "linear: unknown out dtype %d", out_dtype);
+  if (m == 0) return DX_OK;
+  const auto *X = static_cast<const uint16_t *>(x);
+  const auto *W = static_cast<const uint16_t *>(w);
+  hipError_t e = out_dtype == DX_BF16
+                     ? dx_gemm_bf16(X, W, static_cast<uint16_t *>(y), m, n, k, ldx, ldw, ldy, as_stream(stream))
+                     : dx_gemm_f32(X, W, static_cast<float *>(y), m, n, k, ldx, ldw, ldy, as_stream(stream));
+  return check_launch(e, "linear launch");
+}
+
+int dx_gated_linear(const void *x, const void *gate_up, void *act, int64_t m, int64_t f, int64_t k, int64_t ldx,
+                    int64_t ld_act, int32_t activation, void *stream) {
+  REQUIRE(x && gate_up && act, "gated_linear: null pointer argument");
+  REQUIRE(m >= 0 && f > 0 && k > 0, "gated_linear: bad sizes");
+  SUPPORTED(f % 128 == 0, "gated_linear: f=%ld must be a multiple of 128", (long)f);
+  SUPPORTED(k % 64 == 0, "gated_linear: k=%ld must be a multiple of 64", (long)k);
+  REQUIRE(ldx >= k && ld_act >= f && ldx % 8 == 0 && ld_act % 8 == 0, "gated_linear: bad leading dimensions");
+  REQUIRE(aligned16(x) && aligned16(gate_up) && aligned16(act), "gated_linear: pointers must be 16-byte aligned");
+  REQUIRE(activation == DX_ACT_GELU_TANH || activation == DX_ACT_SILU, "gated_linear: unknown activation %d",
+          activation);
+  if (m == 0) return DX_OK;
+  return check_launch(dx_gemm_gated(static_cast<const uint16_t *>(x), static_cast<const uint16_t *>(gate_up),
+                                    static_cast<uint16_t *>(act), m, f, k, ldx, ld_act, activation,
+                                    as_stream(stream)),
+                      "gated_linear launch");
+}
+
+int dx_pack_gate_up(const void *gate, const void *up, void *packed, int64_t f, int64_t k, void *stream) {
+  REQUIRE(gate && up && packed, "pack_gate_up: null pointer argument");
+  SUPPORTED(f % 64 == 0 && f > 0, "pack_gate_up: f=%ld must be a positive multiple of 64", (long)f);
+  REQUIRE(k % 8 == 0 && k > 0, "pack_gate_up: k must be a positive multiple of 8");
+  REQUIRE(aligned16(gate) && aligned16(up) && aligned16(packed), "pack_gate_up: pointers must be 16-byte aligned");
+  return check_launch(dx_pack_gate_up_launch(static_cast<const uint16_t *>(gate), static_cast<const uint16_t *>(up),
+                                             static_cast<uint16_t *>(packed), f, k, as_stream(stream)),
+                      "pack_gate_up launch");
+}
+
+int64_t dx_norm_project_workspace(int64_t rows, int64_t d) { return align_up(rows * d * 2, 256); }
+
+int dx_norm_project(const void *x, const void *norm_w, const uint8_t *row_mask, const void *w, void *y, int64_t rows,
+                    int64_t d, int64_t n, float eps, void *workspace, int64_t workspace_bytes, void *stream) {
+  REQUIRE(x && norm_w && w && y && workspace, "norm_project: null pointer argument");
+  REQUIRE(rows >= 0 && d > 0 && n > 0, "norm_project: bad sizes");
+  SUPPORTED(d % 64 == 0 && d <= 8192, "norm_project: d=%ld must be a multiple of 64 and <= 8192", (long)d);
+  SUPPORTED(n % 256 == 0, "norm_project: n=%ld must be a multiple of 256", (long)n);
+  REQUIRE(workspace_bytes >= dx_norm_project_workspace(rows, d), "norm_project: workspace too small");
+  REQUIRE(aligned16(x) && aligned16(norm_w) && aligned16(w) && aligned16(y) && aligned16(workspace),
+          "norm_project: pointers must be 16-byte aligned");
+  if (rows == 0) return DX_OK;
+  uint16_t *h = static_cast<uint16_t *>(workspace);
+  hipError_t e = dx_rmsnorm_launch(static_cast<const uint16_t *>(x), static_cast<const uint16_t *>(norm_w), h,
+                                   row_mask, rows, (int)d, d, d, eps, as_stream(stream));
+  if (e != hipSuccess) return check_launch(e, "norm_project rmsnorm launch");
+  return check_launch(dx_gemm_bf16(h, static_cast<const uint16_t *>(w), static_cast<uint16_t *>(y), rows, n, d, d, d,
+                                   n, as_stream(stream)),
+                      "norm_project gemm launch");
+}
+
+int64_t dx_mlp_workspace(int64_t rows, int64_t d, int64_t f) {
+  return align_up(rows * d * 2, 256) + align_up(rows * f * 2, 256);
+}
+
+int dx_mlp(const void *x, const void *norm_w, const void *gate_up, const void *down, void *y, int64_t rows, int64_t d,
+           int64_t f, float eps, int32_t activation, int32_t out_dtype, void *workspace, int64_t workspace_bytes,
+           void *stream) {
+  REQUIRE(x && norm_w && gate_up && down && y && workspace, "mlp: null pointer argument");
+  REQUIRE(rows >= 0 && d > 0 && f > 0, "mlp: bad sizes");
+  SUPPORTED(d % 256 == 0 && d <= 8192, "mlp: d=%ld must be a multiple of 256 and <= 8192", (long)d);
+  SUPPORTED(f % 128 == 0, "mlp: f=%ld must be a multiple of 128", (long)f);
+  REQUIRE(activation == DX_ACT_GELU_TANH || activation == DX_ACT_SILU, "mlp: unknown activation %d", activation);
+  REQUIRE(out_dtype == DX_BF16 || out_dtype == DX_F32, "mlp: unknown out dtype %d", out_dtype);
+  REQUIRE(workspace_bytes >= dx_mlp_workspace(rows, d, f), "mlp: workspace too small");
+  REQUIRE(aligned16(x) && aligned16(norm_w) && aligned16(gate_up) && aligned16(down) && aligned16(y) &&
+              aligned16(workspace),
+          "mlp: pointers must be 16-byte aligned");
+  if (rows == 0) return DX_OK;
+  hipStream_t s = as_stream(stream);
+  uint16_t *h = static_cast<uint16_t *>(workspace);
+  uint16_t *a = h + align_up(rows * d * 2, 256) / 2;
+  hipError_t e = dx_rmsnorm_launch(static_cast<const uint16_t *>(x), static_cast<const uint16_t *>(norm_w), h,
+                                   nullptr, rows, (int)d, d, d, eps, s);
+  if (e != hipSuccess) return check_launch(e, "mlp rmsnorm launch");
+  e = dx_gemm_gated(h, static_cast<const uint16_t *>(gate_up), a, rows, f, d, d, f, activation, s);
+  if (e != hipSuccess) return check_launch(e, "mlp gate/up launch");
+  const auto *D = static_cast<const uint16_t *>(down);
+  e = out_dtype == DX_BF16 ? dx_gemm_bf16(a, D, static_cast<uint16_t *>(y), rows, d, f, f, f, d, s)
+                           : dx_gemm_f32(a, D, static_cast<float *>(y), rows, d, f, f, f, d, s);
+  return check_launch(e, "mlp down launch");
+}
+
+int dx_rmsnorm(const void *x, const void *w, void *y, int64_t rows, int64_t d, int64_t ldx, int64_t ldy, float eps,
+               void *stream) {
+  REQUIRE(x && w && y, "rmsnorm: null pointer argument");
+  REQUIRE(rows >= 0 && d > 0 && ldx >= d && ldy >= d, "rmsnorm: bad sizes");
+  SUPPORTED(d % 8 == 0 && d <= 8192, "rmsnorm: d=%ld must be a multiple of 8 and <= 8192", (long)d);
+  REQUIRE(ldx % 8 == 0 && ldy % 8 == 0, "rmsnorm: leading dimensions must be multiples of 8");
+  REQUIRE(aligned16(x) && aligned16(w) && aligned16(y), "rmsnorm: pointers must be 16-byte aligned");
+  if (rows == 0) return DX_OK;
+  return check_launch(dx_rmsnorm_launch(static_cast<const uint16_t *>(x), static_cast<const uint16_t *>(w),
+                                        static_cast<uint16_t *>(y), nullptr, rows, (int)d, ldx, ldy, eps,
+                                        as_stream(stream)),
+                      "rmsnorm launch");
+}
+
+int dx_add_rmsnorm(const void *y, const void *post_w, void *x, const void *next_w, void *h, int64_t rows, int64_t d,
+                   float eps, void *stream) {
+  REQUIRE(y && x, "add_rmsnorm: null pointer argument");
+  REQUIRE((h == nullptr) == (next_w == nullptr), "add_rmsnorm: h and next_w must both be set or both be null");
+  REQUIRE(rows >= 0 && d > 0, "add_rmsnorm: bad sizes");
+  SUPPORTED(d % 8 == 0 && d <= 8192, "add_rmsnorm: d=%ld must be a multiple of 8 and <= 8192", (long)d);
+  REQUIRE(aligned16(y) && aligned16(x) && (!post_w || aligned16(post_w)) && (!h || (aligned16(h) && aligned16(next_w))),
+          "add_rmsnorm: pointers must be 16-byte aligned");
+  if (rows == 0) return DX_OK;
+  return check_launch(dx_add_rmsnorm_launch(static_cast<const uint16_t *>(y), static_cast<const uint16_t *>(post_w),
+                                            static_cast<uint16_t *>(x), static_cast<const uint16_t *>(next_w),
+                                            static_cast<uint16_t *>(h), rows, (int)d, eps, as_stream(stream)),
+                      "add_rmsnorm launch");
+}
+
+int dx_embed(const int32_t *ids, const void *table, void *x, int64_t tokens, int64_t d, int64_t vocab, float scale,
+             const void *norm_w, void *h, float eps, void *stream) {
+  REQUIRE(ids && table && x, "embed: null pointer argument");
+  REQUIRE((h == nullptr) == (norm_w == nullptr), "embed: h and norm_w must both be set or both be null");
+  REQUIRE(tokens >= 0 && d > 0 && vocab > 0, "embed: bad sizes");
+  SUPPORTED(d % 8 == 0 && d <= 8192, "embed: d=%ld must be a multiple of 8 and <= 8192", (long)d);
+  REQUIRE(aligned16(table) && aligned16(x) && (!h || (aligned16(h) && aligned16(norm_w))),
+          "embed: pointers must be 16-byte aligned");
+  if (tokens == 0) return DX_OK;
+  return check_launch(dx_embed_launch(ids, static_cast<const uint16_t *>(table), static_cast<uint16_t *>(x), tokens,
+                                      (int)d, vocab, scale, static_cast<const uint16_t *>(norm_w),
+                                      static_cast<uint16_t *>(h), eps, as_stream(stream)),
+                      "embed launch");
+}
+
+int dx_rope(void *x, const int32_t *positions, const void *cos, const void *sin, int64_t rows, int32_t num_heads,
+            int32_t head_dim, int64_t row_stride, int32_t max_pos, void *stream) {
+  REQUIRE(x && positions && cos && sin, "rope: null pointer argument");
+  REQUIRE(rows >= 0 && num_heads > 0 && max_pos > 0, "rope: bad sizes");
+  SUPPORTED(head_dim % 16 == 0 && head_dim > 0, "rope: head_dim %d must be a multiple of 16", head_dim);
+  REQUIRE(row_stride % 8 == 0 && row_stride >= (int64_t)num_heads * head_dim, "rope: bad row stride");
+  REQUIRE(aligned16(x) && aligned16(cos) && aligned16(sin), "rope: pointers must be 16-byte aligned");
+  if (rows == 0) return DX_OK;
+  return check_launch(dx_rope_launch(static_cast<uint16_t *>(x), positions, static_cast<const uint16_t *>(cos),
+                                     static_cast<const uint16_t *>(sin), rows, num_heads, head_dim, row_stride,
+                                     max_pos, as_stream(stream)),
+                      "rope launch");
+}
+
+int dx_readout(const void *hidden, const void *norm_w, const void *table, const int32_t *opt_pos,
+               const int32_t *opt_label, const int32_t *q_offsets, int32_t num_questions, int64_t num_options,
+               int64_t hidden_rows, int64_t d, int64_t ld_hidden, int64_t vocab, float eps, float softcap,
+               float *logits, float *probs, void *stream) {
+  REQUIRE(hidden && norm_w && table && opt_pos && opt_label && q_offsets && logits && probs,
+          "readout: null pointer argument");
+  REQUIRE(num_questions >= 0 && num_options >= 0 && hidden_rows > 0 && d > 0 && vocab > 0 && ld_hidden >= d,
+          "readout: bad sizes");
+  SUPPORTED(d % 8 == 0 && d <= 8192, "readout: d=%ld must be a multiple of 8 and <= 8192", (long)d);
+  REQUIRE(ld_hidden % 8 == 0, "readout: ld_hidden must be a multiple of 8");
+  REQUIRE(softcap >= 0.f, "readout: softcap must be >= 0");
+  REQUIRE(aligned16(hidden) && aligned16(norm_w) && aligned16(table), "readout: pointers must be 16-byte aligned");
+  if (num_questions == 0) return DX_OK;
+  return check_launch(dx_readout_launch(static_cast<const uint16_t *>(hidden), static_cast<const uint16_t *>(norm_w),
+                                        static_cast<const uint16_t *>(table), opt_pos, opt_label, q_offsets,
+                                        num_questions, hidden_rows, (int)d, ld_hidden, vocab, eps, softcap, logits,
+                                        probs,
+                                        as_stream(stream)),
+                      "readout launch");
+}
+
+}  // extern "C"

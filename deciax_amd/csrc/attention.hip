@@ -1,0 +1,485 @@
+// Causal GQA prefill attention for gfx950 (bf16 MFMA path and an fp32 path).
+//
+// Algorithm (the reference's blocked causal GQA attention,
+// src/deciax/kernels/attention/blocked.py:9-32, in the online form of its TPU
+// flash kernel, src/deciax/kernels/attention/pallas.py:52-135): each
+// workgroup owns one sequence, one KV head and a tile of query rows for all
+// G = Hq / Hkv query heads sharing that KV head, so K/V tiles are staged in LDS
+// once per group instead of being repeated per head (blocked.py:12-13 repeats
+// them). Key tiles entirely outside the causal / sliding window are never
+// visited; only tiles that straddle a boundary evaluate the mask.
+//
+// bf16 path, per wave (32 query rows of one head):
+//   S^T = K Q^T  with 32x32x16 MFMAs: A = K rows from LDS, B = Q^T held in
+//        registers for the whole key loop. Lane l then owns query (l % 32) and
+//        16 keys per 32-key block, so row statistics are lane-local plus one
+//        exchange with lane l ^ 32.
+//   K rows are fed in the order kperm() so that the 8 keys a lane owns in
+//   each half of a 32-key block are consecutive; those 8 scores become, after
+//   bf16 rounding, the lane's B operand of O^T = V^T P^T directly, and the A
+//   operand is one 16-byte read of the V^T tile (V transposed, [D][64] in LDS).
+//
+// Softmax: with logit soft-capping (Gemma-2, cap <= 56) every capped score
+// lies in (-cap, cap), so p = exp(t - cap/2) is computed with a fixed shift:
+// no running max, no rescaling of the O accumulator, no cross-lane max.
+// t - cap/2 = cap/2 - 2 cap / (1 + e^{2x}), x = scale * s / cap, hence
+//   p = exp2(c3 + c2 / (1 + exp2(c1 s))).
+// p stays within [e^{-3cap/2}, e^{cap/2}] — normal fp32 and bf16 numbers for
+// cap <= 56 — and softmax is invariant to the shift. Without soft-capping (or
+// for larger caps) the kernel keeps the usual running max in log2 units.
+// P is rounded to bf16 before P.V (the reference rounds the normalised
+// weights to q.dtype, blocked.py:27); O is divided by the fp32 row sum.
+#include "common.h"
+#include "kernels.h"
+
+namespace {
+
+constexpr int THREADS = 256;
+constexpr int WAVES = 4;
+constexpr int BKV = 64;
+constexpr float LOG2E = 1.4426950408889634f;
+constexpr float NEG_BIG = -1e30f;  // the reference's MASK_FILL (reference.py:8)
+
+enum { MODE_FIXED = 0, MODE_ONLINE = 1 };
+
+DX_DEVICE bool visible(int qi, int key, int len, int window, int causal) {
+  if (key >= len) return false;
+  if (causal) return key <= qi && (window <= 0 || key > qi - window);
+  return window <= 0 || abs(qi - key) <= window;
+}
+
+// K tile in LDS: [64 keys][D], 16-byte chunk c of row r at a swizzled slot.
+template <int D>
+DX_DEVICE int k_off(int row, int chunk) {
+  if constexpr (D / 8 >= 16)
+    return row * D + ((chunk ^ (row & 15)) << 3);
+  else
+    return row * D + ((chunk ^ ((row >> 1) & 7)) << 3);
+}
+
+// V^T tile in LDS: [D][64 keys], 128-byte rows.
+DX_DEVICE int vt_off(int row, int chunk) { return row * 64 + ((chunk ^ ((row >> 1) & 7)) << 3); }
+
+// MFMA row vk of a 32-key block reads key kperm(vk). The output register r of
+// lane-half hh then holds key 16 (r >> 3) + 8 hh + (r & 7).
+DX_DEVICE int kperm(int vk) { return 16 * (vk >> 4) + 8 * ((vk >> 2) & 1) + 4 * ((vk >> 3) & 1) + (vk & 3); }
+
+template <int D, int G, int MODE>
+__global__ void __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(1, 1)))
+attn_bf16_kernel(const uint16_t *__restrict__ Q, const uint16_t *__restrict__ K, const uint16_t *__restrict__ Vt,
+                 uint16_t *__restrict__ O, const int32_t *__restrict__ seq_start,
+                 const int32_t *__restrict__ seq_len, const int32_t *__restrict__ vt_start, long vt_seq_stride,
+                 int max_seq_len, long q_stride, long k_stride, long vt_ld, long o_stride, float scale,
+                 float softcap, int window, int causal) {
+  constexpr int RG = WAVES / G;  // 32-row groups per head
+  constexpr int BQ = 32 * RG;    // query rows per workgroup
+  constexpr int KST = BKV * D;
+  constexpr int STAGE = 2 * BKV * D;
+  constexpr int KCH = BKV * D / 8 / THREADS;
+  constexpr int VCH = D * BKV / 8 / THREADS;
+  constexpr int NKS = D / 16;
+  constexpr int NDB = D / 32;
+  constexpr int CPR = D / 8;  // 16-byte chunks per K row
+  __shared__ __attribute__((aligned(16))) uint16_t smem[2 * STAGE];
+
+  const int b = blockIdx.y, g = blockIdx.z;
+  const int len = min(max(seq_len[b], 0), max_seq_len);
+  const int ntiles = (max_seq_len + BQ - 1) / BQ;
+  const int q0 = (ntiles - 1 - (int)blockIdx.x) * BQ;  // latest (heaviest) tiles launch first
+  if (q0 >= len) return;
+  const long start = seq_start[b];
+  const long vts = vt_start ? (long)vt_start[b] : (long)b * vt_seq_stride;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int lrow = lane & 31, lhalf = lane >> 5;
+  const int rg = wave % RG, h = g * G + wave / RG;
+  const int qw0 = q0 + rg * 32, qw1 = qw0 + 31;
+  const int qi = qw0 + lrow;
+
+  bf16x8 qf[NKS];
+  {
+    const uint16_t *qp = Q + (start + min(qi, len - 1)) * q_stride + (long)h * D + lhalf * 8;
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks) qf[ks] = as_bf16x8(*reinterpret_cast<const u32x4 *>(qp + ks * 16));
+  }
+
+  const int qlast = min(q0 + BQ, len) - 1;
+  int klo, khi;
+  if (causal) {
+    khi = qlast + 1;
+    klo = window > 0 ? max(0, q0 - window + 1) : 0;
+  } else {
+    khi = window > 0 ? min(len, qlast + window + 1) : len;
+    klo = window > 0 ? max(0, q0 - window) : 0;
+  }
+  const int kt0 = klo / BKV, kt1 = (khi + BKV - 1) / BKV;
+
+  const uint16_t *kbase = K + start * k_stride + (long)g * D;
+  const uint16_t *vbase = Vt + (long)g * D * vt_ld + vts;
+  u32x4 rk[KCH], rv[VCH];
+  auto gload = [&](int kt) {
+#pragma unroll
+    for (int j = 0; j < KCH; ++j) {
+      const int id = tid + THREADS * j, row = id / CPR, c = id % CPR;
+      const int key = min(kt * BKV + row, len - 1);
+      rk[j] = *reinterpret_cast<const u32x4 *>(kbase + (long)key * k_stride + c * 8);
+    }
+#pragma unroll
+    for (int j = 0; j < VCH; ++j) {
+      const int id = tid + THREADS * j, row = id >> 3, c = id & 7;
+      rv[j] = *reinterpret_cast<const u32x4 *>(vbase + (long)row * vt_ld + kt * BKV + c * 8);
+    }
+  };
+  auto sstore = [&](int st) {
+    uint16_t *base = smem + st * STAGE;
+#pragma unroll
+    for (int j = 0; j < KCH; ++j) {
+      const int id = tid + THREADS * j, row = id / CPR, c = id % CPR;
+      *reinterpret_cast<u32x4 *>(base + k_off<D>(row, c)) = rk[j];
+    }
+#pragma unroll
+    for (int j = 0; j < VCH; ++j) {
+      const int id = tid + THREADS * j, row = id >> 3, c = id & 7;
+      *reinterpret_cast<u32x4 *>(base + KST + vt_off(row, c)) = rv[j];
+    }
+  };
+
+  floatx16 o[NDB];
+#pragma unroll
+  for (int i = 0; i < NDB; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o[i][r] = 0.f;
+  float lsum = 0.f;
+  float mrun = NEG_BIG;
+
+  const float c1 = 2.f * LOG2E * scale / softcap;
+  const float c2 = -2.f * LOG2E * softcap;
+  const float c3 = 0.5f * LOG2E * softcap;
+
+  gload(kt0);
+  sstore(0);
+  __syncthreads();
+  for (int kt = kt0; kt < kt1; ++kt) {
+    const int st = (kt - kt0) & 1;
+    if (kt + 1 < kt1) gload(kt + 1);
+    const int key0 = kt * BKV;
+
+    bool active = qw0 < len;
+    bool need_mask = key0 + BKV > len;
+    if (causal) {
+      active = active && key0 <= qw1 && !(window > 0 && key0 + BKV - 1 <= qw0 - window);
+      need_mask = need_mask || key0 + BKV - 1 > qw0 || (window > 0 && key0 <= qw1 - window);
+    } else if (window > 0) {
+      active = active && key0 <= qw1 + window && key0 + BKV - 1 >= qw0 - window;
+      need_mask = need_mask || key0 < qw1 - window || key0 + BKV - 1 > qw0 + window;
+    }
+
+    if (active) {
+      const uint16_t *sk = smem + st * STAGE;
+      const uint16_t *sv = sk + KST;
+      floatx16 s[2];
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) s[kb][r] = 0.f;
+        const int krow = kb * 32 + kperm(lrow);
+#pragma unroll
+        for (int ks = 0; ks < NKS; ++ks)
+          s[kb] = mfma32(as_bf16x8(*reinterpret_cast<const u32x4 *>(sk + k_off<D>(krow, ks * 2 + lhalf))), qf[ks],
+                         s[kb]);
+      }
+
+      uint32_t vis = 0xffffffffu;  // bit kb * 16 + r
+      if (need_mask) {
+        vis = 0;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int key = key0 + kb * 32 + 16 * (r >> 3) + 8 * lhalf + (r & 7);
+            vis |= (uint32_t)visible(qi, key, len, window, causal) << (kb * 16 + r);
+          }
+      }
+
+      if constexpr (MODE == MODE_FIXED) {
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const float e = fast_exp2(s[kb][r] * c1);
+            const float p = fast_exp2(c3 + c2 * fast_rcp(1.f + e));
+            s[kb][r] = ((vis >> (kb * 16 + r)) & 1u) ? p : 0.f;
+            lsum += s[kb][r];
+          }
+      } else {
+        float tmax = NEG_BIG;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            float t = s[kb][r] * scale;
+            if (softcap > 0.f) t = softcap * tanhf(t / softcap);
+            t *= LOG2E;
+            t = ((vis >> (kb * 16 + r)) & 1u) ? t : NEG_BIG;
+            s[kb][r] = t;
+            tmax = fmaxf(tmax, t);
+          }
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+        const float mnew = fmaxf(mrun, tmax);
+        const float alpha = fast_exp2(mrun - mnew);
+        mrun = mnew;
+        lsum *= alpha;
+#pragma unroll
+        for (int i = 0; i < NDB; ++i)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) o[i][r] *= alpha;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const float p = ((vis >> (kb * 16 + r)) & 1u) ? fast_exp2(s[kb][r] - mnew) : 0.f;
+            s[kb][r] = p;
+            lsum += p;
+          }
+      }
+
+      bf16x8 pf[4];
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int h2 = 0; h2 < 2; ++h2) {
+          u32x4 w;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) w[i] = pack_bf2(s[kb][8 * h2 + 2 * i], s[kb][8 * h2 + 2 * i + 1]);
+          pf[kb * 2 + h2] = as_bf16x8(w);
+        }
+#pragma unroll
+      for (int db = 0; db < NDB; ++db) {
+        const int vrow = db * 32 + lrow;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int h2 = 0; h2 < 2; ++h2)
+            o[db] = mfma32(as_bf16x8(*reinterpret_cast<const u32x4 *>(sv + vt_off(vrow, kb * 4 + 2 * h2 + lhalf))),
+                           pf[kb * 2 + h2], o[db]);
+      }
+    }
+    if (kt + 1 < kt1) sstore(st ^ 1);
+    __syncthreads();
+  }
+
+  lsum += __shfl_xor(lsum, 32, 64);
+  if (qi < len) {
+    const float inv = 1.f / lsum;
+    uint16_t *op = O + (start + qi) * o_stride + (long)h * D + lhalf * 4;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+      for (int grp = 0; grp < 4; ++grp) {
+        u32x2 w;
+        w[0] = pack_bf2(o[db][grp * 4 + 0] * inv, o[db][grp * 4 + 1] * inv);
+        w[1] = pack_bf2(o[db][grp * 4 + 2] * inv, o[db][grp * 4 + 3] * inv);
+        *reinterpret_cast<u32x2 *>(op + db * 32 + grp * 8) = w;
+      }
+  }
+}
+
+// fp32 path: VALU flash attention, TPQ threads per query row.
+template <int D, int TPQ>
+__global__ void __launch_bounds__(THREADS)
+attn_f32_kernel(const float *__restrict__ Q, const float *__restrict__ K, const float *__restrict__ V,
+                float *__restrict__ O, const int32_t *__restrict__ seq_start, const int32_t *__restrict__ seq_len,
+                int max_seq_len, int hq, int hkv, long q_stride, long k_stride, long v_stride, long o_stride,
+                float scale, float softcap, int window, int causal) {
+  constexpr int QPB = THREADS / TPQ;
+  constexpr int DPT = D / TPQ;
+  constexpr int TK = 32;
+  __shared__ __attribute__((aligned(16))) float ks[TK * D];
+  __shared__ __attribute__((aligned(16))) float vs[TK * D];
+
+  const int b = blockIdx.y, h = blockIdx.z, g = h / (hq / hkv);
+  const int len = min(max(seq_len[b], 0), max_seq_len);
+  const int ntiles = (max_seq_len + QPB - 1) / QPB;
+  const int q0 = (ntiles - 1 - (int)blockIdx.x) * QPB;
+  if (q0 >= len) return;
+  const long start = seq_start[b];
+  const int tid = threadIdx.x, part = tid % TPQ;
+  const int qi = q0 + tid / TPQ;
+
+  float q[DPT], o[DPT];
+  {
+    const float *qp = Q + (start + min(qi, len - 1)) * q_stride + (long)h * D + part * DPT;
+#pragma unroll
+    for (int d = 0; d < DPT; ++d) {
+      q[d] = qp[d];
+      o[d] = 0.f;
+    }
+  }
+  const int qlast = min(q0 + QPB, len) - 1;
+  int klo, khi;
+  if (causal) {
+    khi = qlast + 1;
+    klo = window > 0 ? max(0, q0 - window + 1) : 0;
+  } else {
+    khi = window > 0 ? min(len, qlast + window + 1) : len;
+    klo = window > 0 ? max(0, q0 - window) : 0;
+  }
+  float m = NEG_BIG, l = 0.f;
+  for (int k0 = (klo / TK) * TK; k0 < khi; k0 += TK) {
+    __syncthreads();
+    for (int idx = tid; idx < TK * D / 4; idx += THREADS) {
+      const int row = idx / (D / 4), c = idx % (D / 4);
+      const long key = start + min(k0 + row, len - 1);
+      reinterpret_cast<float4 *>(ks)[idx] = *reinterpret_cast<const float4 *>(K + key * k_stride + (long)g * D + c * 4);
+      reinterpret_cast<float4 *>(vs)[idx] = *reinterpret_cast<const float4 *>(V + key * v_stride + (long)g * D + c * 4);
+    }
+    __syncthreads();
+    float sc[TK];
+    uint32_t vis = 0;
+    float tmax = NEG_BIG;
+#pragma unroll
+    for (int j = 0; j < TK; ++j) {
+      float s = 0.f;
+#pragma unroll
+      for (int d = 0; d < DPT; ++d) s = fmaf(q[d], ks[j * D + part * DPT + d], s);
+#pragma unroll
+      for (int off = 1; off < TPQ; off <<= 1) s += __shfl_xor(s, off, 64);
+      s *= scale;
+      if (softcap > 0.f) s = softcap * tanhf(s / softcap);
+      const bool v = visible(qi, k0 + j, len, window, causal);
+      vis |= (uint32_t)v << j;
+      sc[j] = s;
+      if (v) tmax = fmaxf(tmax, s);
+    }
+    const float mnew = fmaxf(m, tmax);
+    const float alpha = expf(m - mnew);
+    l *= alpha;
+#pragma unroll
+    for (int d = 0; d < DPT; ++d) o[d] *= alpha;
+#pragma unroll
+    for (int j = 0; j < TK; ++j) {
+      const float p = ((vis >> j) & 1u) ? expf(sc[j] - mnew) : 0.f;
+      l += p;
+#pragma unroll
+      for (int d = 0; d < DPT; ++d) o[d] = fmaf(p, vs[j * D + part * DPT + d], o[d]);
+    }
+    m = mnew;
+  }
+  if (qi < len) {
+    float *op = O + (start + qi) * o_stride + (long)h * D + part * DPT;
+    const float inv = 1.f / l;
+#pragma unroll
+    for (int d = 0; d < DPT; ++d) op[d] = o[d] * inv;
+  }
+}
+
+// V rows -> V^T tiles. Grid: (64-row tiles of the longest sequence, sequences,
+// kv heads x D/64). Rows past seq_len up to the next multiple of 64 are
+// written as zeros, so P.V never multiplies a zero probability by stale data.
+__global__ void __launch_bounds__(THREADS)
+transpose_v_kernel(const uint16_t *__restrict__ V, uint16_t *__restrict__ Vt, const int32_t *__restrict__ seq_start,
+                   const int32_t *__restrict__ seq_len, const int32_t *__restrict__ vt_start, long vt_seq_stride,
+                   int max_seq_len, int d, long v_stride, long vt_ld) {
+  __shared__ uint16_t tile[64][66];
+  const int b = blockIdx.y;
+  const int len = min(max(seq_len[b], 0), max_seq_len);
+  const int p0 = blockIdx.x * 64;
+  if (p0 >= len) return;
+  const int dblocks = d / 64;
+  const int g = blockIdx.z / dblocks, d0 = (blockIdx.z % dblocks) * 64;
+  const long start = seq_start[b];
+  const long vts = vt_start ? (long)vt_start[b] : (long)b * vt_seq_stride;
+  const int tid = threadIdx.x;
+  {
+    const int row = tid >> 2, c = (tid & 3) * 16;
+    u32x4 a = {0, 0, 0, 0}, bb = {0, 0, 0, 0};
+    if (p0 + row < len) {
+      const uint16_t *src = V + (start + p0 + row) * v_stride + (long)g * d + d0 + c;
+      a = *reinterpret_cast<const u32x4 *>(src);
+      bb = *reinterpret_cast<const u32x4 *>(src + 8);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      tile[row][c + 2 * i] = (uint16_t)(a[i] & 0xffff);
+      tile[row][c + 2 * i + 1] = (uint16_t)(a[i] >> 16);
+      tile[row][c + 8 + 2 * i] = (uint16_t)(bb[i] & 0xffff);
+      tile[row][c + 8 + 2 * i + 1] = (uint16_t)(bb[i] >> 16);
+    }
+  }
+  __syncthreads();
+  {
+    const int dr = tid >> 2, c = (tid & 3) * 16;
+    u32x4 a, bb;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      a[i] = (uint32_t)tile[c + 2 * i][dr] | ((uint32_t)tile[c + 2 * i + 1][dr] << 16);
+      bb[i] = (uint32_t)tile[c + 8 + 2 * i][dr] | ((uint32_t)tile[c + 8 + 2 * i + 1][dr] << 16);
+    }
+    uint16_t *dst = Vt + ((long)g * d + d0 + dr) * vt_ld + vts + p0 + c;
+    *reinterpret_cast<u32x4 *>(dst) = a;
+    *reinterpret_cast<u32x4 *>(dst + 8) = bb;
+  }
+}
+
+template <int D, int G>
+hipError_t launch_bf16_dg(const AttnArgs &a, hipStream_t s) {
+  constexpr int BQ = 32 * (WAVES / G);
+  const dim3 grid((a.max_seq_len + BQ - 1) / BQ, a.num_seqs, a.hkv);
+  const bool fixed = a.softcap > 0.f && a.softcap <= 56.f;
+  auto kern = fixed ? attn_bf16_kernel<D, G, MODE_FIXED> : attn_bf16_kernel<D, G, MODE_ONLINE>;
+  kern<<<grid, dim3(THREADS), 0, s>>>(
+      static_cast<const uint16_t *>(a.q), static_cast<const uint16_t *>(a.k), static_cast<const uint16_t *>(a.v),
+      static_cast<uint16_t *>(a.out), a.seq_start, a.seq_len, a.vt_start, a.vt_seq_stride, a.max_seq_len,
+      a.q_stride, a.k_stride, a.v_stride, a.out_stride, a.scale, a.softcap, a.window, a.causal);
+  return hipGetLastError();
+}
+
+template <int D>
+hipError_t launch_bf16_d(const AttnArgs &a, hipStream_t s) {
+  switch (a.hq / a.hkv) {
+    case 1: return launch_bf16_dg<D, 1>(a, s);
+    case 2: return launch_bf16_dg<D, 2>(a, s);
+    case 4: return launch_bf16_dg<D, 4>(a, s);
+  }
+  return hipErrorInvalidValue;
+}
+
+template <int D, int TPQ>
+hipError_t launch_f32_d(const AttnArgs &a, hipStream_t s) {
+  constexpr int QPB = THREADS / TPQ;
+  const dim3 grid((a.max_seq_len + QPB - 1) / QPB, a.num_seqs, a.hq);
+  attn_f32_kernel<D, TPQ><<<grid, dim3(THREADS), 0, s>>>(
+      static_cast<const float *>(a.q), static_cast<const float *>(a.k), static_cast<const float *>(a.v),
+      static_cast<float *>(a.out), a.seq_start, a.seq_len, a.max_seq_len, a.hq, a.hkv, a.q_stride, a.k_stride,
+      a.v_stride, a.out_stride, a.scale, a.softcap, a.window, a.causal);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t dx_attn_bf16(const AttnArgs &a, hipStream_t s) {
+  switch (a.d) {
+    case 64: return launch_bf16_d<64>(a, s);
+    case 128: return launch_bf16_d<128>(a, s);
+    case 256: return launch_bf16_d<256>(a, s);
+  }
+  return hipErrorInvalidValue;
+}
+
+hipError_t dx_attn_f32(const AttnArgs &a, hipStream_t s) {
+  switch (a.d) {
+    case 64: return launch_f32_d<64, 1>(a, s);
+    case 128: return launch_f32_d<128, 2>(a, s);
+    case 256: return launch_f32_d<256, 4>(a, s);
+  }
+  return hipErrorInvalidValue;
+}
+
+hipError_t dx_transpose_v_launch(const uint16_t *v, uint16_t *vt, const int32_t *seq_start, const int32_t *seq_len,
+                                 const int32_t *vt_start, long vt_seq_stride, int num_seqs, int max_seq_len, int hkv,
+                                 int d, long v_stride, long vt_ld, hipStream_t s) {
+  const dim3 grid((max_seq_len + 63) / 64, num_seqs, hkv * (d / 64));
+  transpose_v_kernel<<<grid, dim3(THREADS), 0, s>>>(v, vt, seq_start, seq_len, vt_start, vt_seq_stride, max_seq_len,
+                                                   d, v_stride, vt_ld);
+  return hipGetLastError();
+}

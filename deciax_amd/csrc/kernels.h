@@ -1,0 +1,46 @@
+// Internal launchers shared between the kernel files and the C ABI layer.
+// Shapes are validated by the ABI layer before any of these is called.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+hipError_t dx_gemm_bf16(const uint16_t *A, const uint16_t *B, uint16_t *C, long M, long N, long K, long lda,
+                        long ldb, long ldc, hipStream_t s);
+hipError_t dx_gemm_f32(const uint16_t *A, const uint16_t *B, float *C, long M, long N, long K, long lda, long ldb,
+                       long ldc, hipStream_t s);
+hipError_t dx_gemm_gated(const uint16_t *A, const uint16_t *B, uint16_t *C, long M, long F, long K, long lda,
+                         long ldc, int act, hipStream_t s);
+
+struct AttnArgs {
+  const void *q, *k, *v;  // v: token-major (fp32 path) or transposed (bf16 path)
+  void *out;
+  const int32_t *seq_start, *seq_len, *vt_start;
+  int num_seqs, max_seq_len, hq, hkv, d;
+  long q_stride, k_stride, v_stride, out_stride;  // v_stride = vt_ld on the bf16 path
+  long vt_seq_stride;                              // used when vt_start == nullptr
+  float scale, softcap;
+  int window, causal;
+};
+
+hipError_t dx_attn_bf16(const AttnArgs &a, hipStream_t s);
+hipError_t dx_attn_f32(const AttnArgs &a, hipStream_t s);
+hipError_t dx_transpose_v_launch(const uint16_t *v, uint16_t *vt, const int32_t *seq_start, const int32_t *seq_len,
+                                 const int32_t *vt_start, long vt_seq_stride, int num_seqs, int max_seq_len, int hkv,
+                                 int d, long v_stride, long vt_ld, hipStream_t s);
+
+hipError_t dx_rmsnorm_launch(const uint16_t *x, const uint16_t *w, uint16_t *y, const uint8_t *mask, long rows,
+                             int d, long ldx, long ldy, float eps, hipStream_t s);
+hipError_t dx_add_rmsnorm_launch(const uint16_t *y, const uint16_t *post_w, uint16_t *x, const uint16_t *next_w,
+                                 uint16_t *h, long rows, int d, float eps, hipStream_t s);
+hipError_t dx_embed_launch(const int32_t *ids, const uint16_t *table, uint16_t *x, long tokens, int d, long vocab,
+                           float scale, const uint16_t *norm_w, uint16_t *h, float eps, hipStream_t s);
+hipError_t dx_rope_launch(uint16_t *x, const int32_t *pos, const uint16_t *cos, const uint16_t *sin, long rows,
+                          int heads, int d, long stride, int max_pos, hipStream_t s);
+hipError_t dx_readout_launch(const uint16_t *hidden, const uint16_t *norm_w, const uint16_t *table,
+                             const int32_t *opt_pos, const int32_t *opt_label, const int32_t *q_off, int nq,
+                             long hidden_rows, int d,
+                             long ld_hidden, long vocab, float eps, float softcap, float *logits, float *probs,
+                             hipStream_t s);
+hipError_t dx_pack_gate_up_launch(const uint16_t *gate, const uint16_t *up, uint16_t *packed, long f, long k,
+                                  hipStream_t s);

@@ -1,0 +1,345 @@
+"""Typed host wrappers over the C ABI, on torch device tensors.
+
+torch provides device memory and the current HIP stream; every computation
+runs in the gfx950 kernels of `libdeciax_hip.so`. Wrappers validate shapes,
+dtypes and devices on the host (raising ValueError, like the reference's
+kernel wrappers, e.g. src/deciax/kernels/projection.py:22-26) and then launch
+asynchronously on `torch.cuda.current_stream()`.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from collections.abc import Sequence
+
+import torch
+
+from deciax_amd import _lib
+from deciax_amd._lib import DX_ACT_GELU_TANH, DX_ACT_SILU, DX_BF16, DX_F32, call
+
+BF16 = torch.bfloat16
+F32 = torch.float32
+ACTIVATIONS = {"gelu_tanh": DX_ACT_GELU_TANH, "gelu_pytorch_tanh": DX_ACT_GELU_TANH, "silu": DX_ACT_SILU}
+
+
+def _ptr(t: torch.Tensor | None) -> ctypes.c_void_p | None:
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream() -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _need(t: torch.Tensor, name: str, dtype: torch.dtype, ndim: int | None = None) -> None:
+    if not isinstance(t, torch.Tensor):
+        raise ValueError(f"{name} must be a torch.Tensor")
+    if t.device.type != "cuda":
+        raise ValueError(f"{name} must be a device (HIP) tensor, got {t.device}")
+    if t.dtype != dtype:
+        raise ValueError(f"{name} must be {dtype}, got {t.dtype}")
+    if ndim is not None and t.dim() != ndim:
+        raise ValueError(f"{name} must have {ndim} dims, got shape {tuple(t.shape)}")
+
+
+def _rows(t: torch.Tensor, name: str) -> int:
+    """Row stride of a 2-D view whose rows are contiguous."""
+    if t.stride(-1) != 1:
+        raise ValueError(f"{name} rows must be contiguous")
+    return t.stride(0)
+
+
+def _activation(act: str) -> int:
+    try:
+        return ACTIVATIONS[act]
+    except KeyError:
+        raise ValueError(f"activation must be one of {sorted(ACTIVATIONS)}, got {act!r}") from None
+
+
+# ---------------------------------------------------------------------------- projections
+
+
+def linear(x: torch.Tensor, w: torch.Tensor, *, out: torch.Tensor | None = None,
+           out_dtype: torch.dtype = BF16) -> torch.Tensor:
+    """`x @ w.T` for a PyTorch-layout [out, in] weight (src/deciax/nn.py:11-19), bf16 operands,
+    fp32 accumulation, result rounded once to `out_dtype`."""
+    _need(x, "x", BF16, 2)
+    _need(w, "w", BF16, 2)
+    m, k = x.shape
+    n = w.shape[0]
+    if w.shape[1] != k:
+        raise ValueError(f"linear: x {tuple(x.shape)} and w {tuple(w.shape)} disagree on k")
+    if out is None:
+        out = torch.empty((m, n), dtype=out_dtype, device=x.device)
+    _need(out, "out", out_dtype, 2)
+    if tuple(out.shape) != (m, n):
+        raise ValueError(f"linear: out must be {(m, n)}, got {tuple(out.shape)}")
+    code = {BF16: DX_BF16, F32: DX_F32}.get(out_dtype)
+    if code is None:
+        raise ValueError(f"linear: out_dtype must be bf16 or fp32, got {out_dtype}")
+    call("dx_linear", _ptr(x), _ptr(w), _ptr(out), m, n, k, _rows(x, "x"), _rows(w, "w"), _rows(out, "out"), code,
+         _stream())
+    return out
+
+
+def pack_gate_up(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
+    """[f, k] gate and up weights -> the [2f, k] packed layout of `gated_linear`
+    (the role of `pack`, src/deciax/kernels/swiglu.py:45-51)."""
+    _need(gate, "gate", BF16, 2)
+    _need(up, "up", BF16, 2)
+    if gate.shape != up.shape:
+        raise ValueError("gate and up must have the same shape")
+    f, k = gate.shape
+    gate, up = gate.contiguous(), up.contiguous()
+    packed = torch.empty((2 * f, k), dtype=BF16, device=gate.device)
+    call("dx_pack_gate_up", _ptr(gate), _ptr(up), _ptr(packed), f, k, _stream())
+    return packed
+
+
+def gated_linear(x: torch.Tensor, gate_up: torch.Tensor, activation: str = "gelu_tanh", *,
+                 out: torch.Tensor | None = None) -> torch.Tensor:
+    """act(x @ gate.T) * (x @ up.T) with the reference's bf16 rounding points
+    (src/deciax/kernels/swiglu.py:100-101)."""
+    _need(x, "x", BF16, 2)
+    _need(gate_up, "gate_up", BF16, 2)
+    m, k = x.shape
+    f2, kw = gate_up.shape
+    if kw != k or f2 % 2:
+        raise ValueError(f"gated_linear: x {tuple(x.shape)} and gate_up {tuple(gate_up.shape)} disagree")
+    f = f2 // 2
+    if out is None:
+        out = torch.empty((m, f), dtype=BF16, device=x.device)
+    _need(out, "out", BF16, 2)
+    call("dx_gated_linear", _ptr(x), _ptr(gate_up), _ptr(out), m, f, k, _rows(x, "x"), _rows(out, "out"),
+         _activation(activation), _stream())
+    return out
+
+
+def norm_project(x: torch.Tensor, norm: torch.Tensor, weight: torch.Tensor, *, eps: float,
+                 row_mask: torch.Tensor | None = None) -> torch.Tensor:
+    """RMSNorm(1 + w) -> optional row mask -> packed projection [n, d]
+    (`norm_project`, src/deciax/kernels/projection.py:13-53)."""
+    _need(x, "x", BF16, 2)
+    _need(norm, "norm", BF16, 1)
+    _need(weight, "weight", BF16, 2)
+    rows, d = x.shape
+    n = weight.shape[0]
+    if weight.shape[1] != d or norm.shape[0] != d:
+        raise ValueError("norm_project: hidden sizes disagree")
+    x = x.contiguous()
+    mask_u8 = None
+    if row_mask is not None:
+        if row_mask.shape != (rows,):
+            raise ValueError("norm_project: row_mask must be [rows]")
+        mask_u8 = row_mask.to(device=x.device, dtype=torch.uint8).contiguous()
+    ws_bytes = _lib.lib().dx_norm_project_workspace(rows, d)
+    ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=x.device)
+    y = torch.empty((rows, n), dtype=BF16, device=x.device)
+    call("dx_norm_project", _ptr(x), _ptr(norm.contiguous()), _ptr(mask_u8), _ptr(weight.contiguous()), _ptr(y), rows,
+         d, n, float(eps), _ptr(ws), ws.numel(), _stream())
+    return y
+
+
+def mlp(x: torch.Tensor, norm: torch.Tensor, gate_up: torch.Tensor, down: torch.Tensor, *, eps: float,
+        activation: str = "gelu_tanh", out_dtype: torch.dtype = F32) -> torch.Tensor:
+    """RMSNorm(1 + w) -> gated gate|up -> down with fp32 accumulation over all of f
+    (`fused_mlp_partial`, src/deciax/kernels/swiglu.py:166-208). `down` is [d, f]."""
+    _need(x, "x", BF16, 2)
+    _need(norm, "norm", BF16, 1)
+    _need(gate_up, "gate_up", BF16, 2)
+    _need(down, "down", BF16, 2)
+    rows, d = x.shape
+    f = gate_up.shape[0] // 2
+    if gate_up.shape != (2 * f, d) or down.shape != (d, f) or norm.shape != (d,):
+        raise ValueError("mlp: inconsistent packed MLP shapes")
+    code = {BF16: DX_BF16, F32: DX_F32}.get(out_dtype)
+    if code is None:
+        raise ValueError("mlp: out_dtype must be bf16 or fp32")
+    x = x.contiguous()
+    ws_bytes = _lib.lib().dx_mlp_workspace(rows, d, f)
+    ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=x.device)
+    y = torch.empty((rows, d), dtype=out_dtype, device=x.device)
+    call("dx_mlp", _ptr(x), _ptr(norm.contiguous()), _ptr(gate_up.contiguous()), _ptr(down.contiguous()), _ptr(y),
+         rows, d, f, float(eps), _activation(activation), code, _ptr(ws), ws.numel(), _stream())
+    return y
+
+
+# ---------------------------------------------------------------------------- norms, embedding, rope
+
+
+def rmsnorm(x: torch.Tensor, w: torch.Tensor, *, eps: float, out: torch.Tensor | None = None) -> torch.Tensor:
+    """`rms` of src/deciax/models/qwen3_5/text.py:25-28 over the last dim of a 2-D tensor."""
+    _need(x, "x", BF16, 2)
+    _need(w, "w", BF16, 1)
+    rows, d = x.shape
+    if out is None:
+        out = torch.empty_like(x)
+    call("dx_rmsnorm", _ptr(x), _ptr(w), _ptr(out), rows, d, _rows(x, "x"), _rows(out, "out"), float(eps), _stream())
+    return out
+
+
+def add_rmsnorm(y: torch.Tensor, x: torch.Tensor, *, eps: float, post_w: torch.Tensor | None = None,
+                next_w: torch.Tensor | None = None, h: torch.Tensor | None = None) -> torch.Tensor | None:
+    """In place x = x + (post-normed) y; returns h = rms(x)(1 + next_w) when next_w is given."""
+    _need(y, "y", BF16, 2)
+    _need(x, "x", BF16, 2)
+    if y.shape != x.shape or not (x.is_contiguous() and y.is_contiguous()):
+        raise ValueError("add_rmsnorm: y and x must be contiguous and of one shape")
+    rows, d = x.shape
+    if next_w is not None and h is None:
+        h = torch.empty_like(x)
+    call("dx_add_rmsnorm", _ptr(y), _ptr(post_w), _ptr(x), _ptr(next_w), _ptr(h if next_w is not None else None),
+         rows, d, float(eps), _stream())
+    return h if next_w is not None else None
+
+
+def embed(ids: torch.Tensor, table: torch.Tensor, *, scale: float = 1.0, norm_w: torch.Tensor | None = None,
+          eps: float = 1e-6, x: torch.Tensor | None = None,
+          h: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor | None]:
+    """Embedding gather times a bf16 scale (`_embed`, src/deciax/models/clef/model.py:81), plus the
+    first layer's input norm when `norm_w` is given."""
+    _need(ids, "ids", torch.int32, 1)
+    _need(table, "table", BF16, 2)
+    vocab, d = table.shape
+    if x is None:
+        x = torch.empty((ids.shape[0], d), dtype=BF16, device=table.device)
+    if norm_w is not None and h is None:
+        h = torch.empty_like(x)
+    for t, n in ((x, "x"), (h, "h")):
+        if t is not None and (tuple(t.shape) != (ids.shape[0], d) or not t.is_contiguous()):
+            raise ValueError(f"embed: {n} must be a contiguous [tokens, d] tensor")
+    h = h if norm_w is not None else None
+    call("dx_embed", _ptr(ids.contiguous()), _ptr(table), _ptr(x), ids.shape[0], d, vocab, float(scale),
+         _ptr(norm_w), _ptr(h), float(eps), _stream())
+    return x, h
+
+
+def rope(x: torch.Tensor, positions: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, *, num_heads: int,
+         head_dim: int) -> torch.Tensor:
+    """In-place rotate-half RoPE on the first `num_heads` heads of each row of a 2-D
+    [rows, >= num_heads * head_dim] tensor (`apply_rope`, src/deciax/nn.py:35-44)."""
+    _need(x, "x", BF16, 2)
+    _need(positions, "positions", torch.int32, 1)
+    _need(cos, "cos", BF16, 2)
+    _need(sin, "sin", BF16, 2)
+    if cos.shape != sin.shape or cos.shape[1] != head_dim // 2:
+        raise ValueError("rope: cos/sin tables must be [max_pos, head_dim / 2]")
+    if positions.shape[0] != x.shape[0]:
+        raise ValueError("rope: one position per row")
+    call("dx_rope", _ptr(x), _ptr(positions), _ptr(cos), _ptr(sin), x.shape[0], num_heads, head_dim,
+         _rows(x, "x"), cos.shape[0], _stream())
+    return x
+
+
+# ---------------------------------------------------------------------------- attention
+
+
+def attention_varlen(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, seq_start: torch.Tensor,
+                     seq_len: torch.Tensor, max_seq_len: int, *, num_q_heads: int, num_kv_heads: int, head_dim: int,
+                     scale: float, softcap: float = 0.0, window: int = 0, causal: bool = True,
+                     out: torch.Tensor | None = None) -> torch.Tensor:
+    """Prefill attention over packed rows: q [rows, >= Hq*D], k/v [rows, >= Hkv*D] (2-D views with
+    contiguous rows, possibly column slices of one packed qkv buffer). bf16 or fp32."""
+    dtype = q.dtype
+    if dtype not in (BF16, F32):
+        raise ValueError(f"attention: dtype must be bf16 or fp32, got {dtype}")
+    for t, n in ((q, "q"), (k, "k"), (v, "v")):
+        _need(t, n, dtype, 2)
+    _need(seq_start, "seq_start", torch.int32, 1)
+    _need(seq_len, "seq_len", torch.int32, 1)
+    if out is None:
+        out = torch.empty((q.shape[0], num_q_heads * head_dim), dtype=dtype, device=q.device)
+    _need(out, "out", dtype, 2)
+    nseq = seq_start.shape[0]
+    code = DX_BF16 if dtype == BF16 else DX_F32
+    ws_bytes = _lib.lib().dx_attn_prefill_workspace(nseq, max_seq_len, num_kv_heads, head_dim, code)
+    ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=q.device)
+    call("dx_attn_prefill", _ptr(q), _ptr(k), _ptr(v), _ptr(out), _ptr(seq_start), _ptr(seq_len), nseq, max_seq_len,
+         num_q_heads, num_kv_heads, head_dim, _rows(q, "q"), _rows(k, "k"), _rows(v, "v"), _rows(out, "out"),
+         float(scale), float(softcap), int(window), int(bool(causal)), code, _ptr(ws), ws.numel(), _stream())
+    return out
+
+
+def transpose_v(v: torch.Tensor, vt: torch.Tensor, seq_start: torch.Tensor, seq_len: torch.Tensor,
+                vt_start: torch.Tensor, max_seq_len: int, *, num_kv_heads: int, head_dim: int) -> torch.Tensor:
+    _need(v, "v", BF16, 2)
+    _need(vt, "vt", BF16, 2)
+    call("dx_transpose_v", _ptr(v), _ptr(vt), _ptr(seq_start), _ptr(seq_len), _ptr(vt_start), seq_start.shape[0],
+         max_seq_len, num_kv_heads, head_dim, _rows(v, "v"), _rows(vt, "vt"), _stream())
+    return vt
+
+
+def attention_vt(q: torch.Tensor, k: torch.Tensor, vt: torch.Tensor, seq_start: torch.Tensor, seq_len: torch.Tensor,
+                 vt_start: torch.Tensor, max_seq_len: int, *, num_q_heads: int, num_kv_heads: int, head_dim: int,
+                 scale: float, softcap: float = 0.0, window: int = 0, causal: bool = True,
+                 out: torch.Tensor | None = None) -> torch.Tensor:
+    """bf16 attention with V pre-transposed by `transpose_v` (the model driver's form)."""
+    for t, n in ((q, "q"), (k, "k"), (vt, "vt")):
+        _need(t, n, BF16, 2)
+    if out is None:
+        out = torch.empty((q.shape[0], num_q_heads * head_dim), dtype=BF16, device=q.device)
+    call("dx_attn_prefill_vt", _ptr(q), _ptr(k), _ptr(vt), _ptr(out), _ptr(seq_start), _ptr(seq_len),
+         _ptr(vt_start), seq_start.shape[0], max_seq_len, num_q_heads, num_kv_heads, head_dim, _rows(q, "q"),
+         _rows(k, "k"), _rows(vt, "vt"), _rows(out, "out"), float(scale), float(softcap), int(window),
+         int(bool(causal)), _stream())
+    return out
+
+
+def _prefix_lengths(key_mask: torch.Tensor) -> torch.Tensor:
+    """Lengths of right-padded [B, S] masks; other masks are rejected."""
+    m = key_mask.to(torch.bool)
+    lengths = m.sum(dim=1, dtype=torch.int32)
+    pos = torch.arange(m.shape[1], device=m.device)[None, :]
+    if not bool(torch.equal(m, pos < lengths[:, None])):
+        raise ValueError("attention: key_mask must mark a prefix of each row (right padding)")
+    return lengths
+
+
+def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, key_mask: torch.Tensor, *, causal: bool = False,
+              window: int = 0, softcap: float = 0.0, scale: float | None = None) -> torch.Tensor:
+    """[B, S, H, D] q and [B, S, Hkv, D] k, v with a right-padded [B, S] key mask -> [B, S, H, D].
+
+    The interface of `blocked.attention` (src/deciax/kernels/attention/blocked.py:9) and, with
+    `causal=False`, of `ops.attention` (src/deciax/ops/__init__.py:10-26): rows past a sequence's
+    length are left zero (the reference computes them but never reads them,
+    tests/kernels/test_attention.py:42)."""
+    if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
+        raise ValueError("attention: q, k, v must be [B, S, H, D]")
+    b, s, hq, d = q.shape
+    hkv = k.shape[2]
+    if k.shape != (b, s, hkv, d) or v.shape != k.shape or key_mask.shape != (b, s):
+        raise ValueError("attention: inconsistent q/k/v/mask shapes")
+    lengths = _prefix_lengths(key_mask.to(q.device))
+    starts = torch.arange(b, device=q.device, dtype=torch.int32) * s
+    out = torch.zeros((b * s, hq * d), dtype=q.dtype, device=q.device)
+    attention_varlen(q.reshape(b * s, hq * d).contiguous(), k.reshape(b * s, hkv * d).contiguous(),
+                     v.reshape(b * s, hkv * d).contiguous(), starts, lengths, s, num_q_heads=hq, num_kv_heads=hkv,
+                     head_dim=d, scale=d ** -0.5 if scale is None else scale, softcap=softcap, window=window,
+                     causal=causal, out=out)
+    return out.reshape(b, s, hq, d)
+
+
+# ---------------------------------------------------------------------------- readout
+
+
+def readout(hidden: torch.Tensor, norm_w: torch.Tensor, table: torch.Tensor, opt_pos: torch.Tensor,
+            opt_label: torch.Tensor, q_offsets: torch.Tensor, *, eps: float,
+            softcap: float = 0.0) -> tuple[torch.Tensor, torch.Tensor]:
+    """Option logits and per-question probabilities (see dx_readout)."""
+    _need(hidden, "hidden", BF16, 2)
+    _need(norm_w, "norm_w", BF16, 1)
+    _need(table, "table", BF16, 2)
+    for t, n in ((opt_pos, "opt_pos"), (opt_label, "opt_label"), (q_offsets, "q_offsets")):
+        _need(t, n, torch.int32, 1)
+    nopt = opt_pos.shape[0]
+    logits = torch.empty(nopt, dtype=F32, device=hidden.device)
+    probs = torch.empty(nopt, dtype=F32, device=hidden.device)
+    nq = q_offsets.shape[0] - 1
+    call("dx_readout", _ptr(hidden), _ptr(norm_w), _ptr(table), _ptr(opt_pos), _ptr(opt_label), _ptr(q_offsets),
+         nq, nopt, hidden.shape[0], hidden.shape[1], _rows(hidden, "hidden"), table.shape[0], float(eps),
+         float(softcap),
+         _ptr(logits), _ptr(probs), _stream())
+    return logits, probs
+
+
+def int32_device(values: Sequence[int] | torch.Tensor, device: torch.device | str) -> torch.Tensor:
+    return torch.as_tensor(values, dtype=torch.int32).to(device)

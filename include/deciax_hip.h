@@ -1,0 +1,236 @@
+/*
+ * deciax_hip.h — C ABI of the MI355X (gfx950) decision-prefill kernels.
+ *
+ * Every entry point takes plain device pointers, int64 sizes and strides in
+ * elements, fp32 scalars and a `hipStream_t` passed as `void *`. Calls are
+ * stream-ordered and asynchronous: nothing allocates device memory and nothing
+ * synchronises the host. The caller owns every buffer; entry points that need
+ * scratch memory take a caller-provided workspace whose size comes from the
+ * matching `*_workspace` query. Calls are thread-safe given distinct output
+ * buffers (the library keeps no mutable device state).
+ *
+ * Return value: DX_OK, or a status code; `dx_last_error()` then holds a
+ * message for the calling thread. DX_ERR_INVALID and DX_ERR_UNSUPPORTED mean
+ * the arguments were rejected before any launch (the Python layer raises
+ * ValueError, which the reference's HTTP layer maps to 422 —
+ * src/deciax/serve/app.py:260-261); DX_ERR_RUNTIME is a HIP launch/runtime
+ * failure (RuntimeError, mapped to 500 at src/deciax/serve/app.py:262-264).
+ *
+ * Reference interfaces replaced (paths relative to the deciax checkout):
+ * each declaration names the function whose contract it takes over.
+ */
+#ifndef DECIAX_HIP_H
+#define DECIAX_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum dx_status {
+  DX_OK = 0,
+  DX_ERR_INVALID = 1,     /* bad shape, stride, alignment, dtype or null pointer */
+  DX_ERR_UNSUPPORTED = 2, /* well-formed but outside what the kernels implement */
+  DX_ERR_RUNTIME = 3,     /* HIP runtime or launch failure */
+};
+
+enum dx_dtype { DX_BF16 = 0, DX_F32 = 1 };
+
+enum dx_activation { DX_ACT_GELU_TANH = 0, DX_ACT_SILU = 1 };
+
+/* Library identification and the calling thread's last error message. */
+const char *dx_version(void);
+const char *dx_last_error(void);
+
+/* gfx architecture name of `device` (e.g. "gfx950") into buf; DX_OK or
+ * DX_ERR_RUNTIME. Used by the impl resolver, which requires gfx950
+ * (src/deciax/ops/backend.py:13-18 resolves impls; src/deciax/models/clef/model.py:46-50
+ * rejects an impl whose device is missing). */
+int dx_device_arch(int device, char *buf, int buf_len);
+
+/* ------------------------------------------------------------------------ */
+/* Attention                                                                 */
+/* ------------------------------------------------------------------------ */
+
+/* Causal (or bidirectional) GQA prefill attention over variable-length
+ * sequences. Replaces `attention` in src/deciax/kernels/attention/blocked.py:9-32
+ * (causal GQA, fp32 scores, softmax, P.V) and the masked forms of
+ * src/deciax/kernels/attention/reference.py:20-42 and
+ * src/deciax/kernels/attention/pallas.py:52-135, extended with Gemma-2 logit
+ * soft-capping and the causal sliding window.
+ *
+ * Sequence s occupies rows [seq_start[s], seq_start[s] + seq_len[s]) of q, k,
+ * v and out (device int32 arrays). Row r, head h lives at
+ * base + r * row_stride + h * head_dim. The padded [B, S, H, D] layout with a
+ * right-padded key mask is the case seq_start[s] = s * S.
+ *
+ * scores = scale * q.k; if softcap > 0, scores = softcap * tanh(scores / softcap);
+ * causal: key j is visible to query i iff j <= i and (window == 0 or j > i - window);
+ * bidirectional (causal == 0): iff window == 0 or |i - j| <= window.
+ * Softmax in fp32; bf16 P.V with fp32 accumulation (dtype DX_BF16), or fp32
+ * throughout (DX_F32). Rows past seq_len are never written.
+ *
+ * bf16 requires head_dim in {64, 128, 256} and num_q_heads / num_kv_heads in
+ * {1, 2, 4}; fp32 requires head_dim in {64, 128, 256}. The bf16 path stages V
+ * transposed in `workspace` (size from dx_attn_prefill_workspace with the
+ * same num_seqs and max_seq_len; the fp32 path needs none). Every seq_len must
+ * be <= max_seq_len (longer ones are cut to max_seq_len). */
+int dx_attn_prefill(const void *q, const void *k, const void *v, void *out,
+                    const int32_t *seq_start, const int32_t *seq_len,
+                    int32_t num_seqs, int32_t max_seq_len, int32_t num_q_heads,
+                    int32_t num_kv_heads, int32_t head_dim, int64_t q_row_stride,
+                    int64_t k_row_stride, int64_t v_row_stride,
+                    int64_t out_row_stride, float scale, float softcap,
+                    int32_t window, int32_t causal, int32_t dtype,
+                    void *workspace, int64_t workspace_bytes, void *stream);
+
+int64_t dx_attn_prefill_workspace(int32_t num_seqs, int32_t max_seq_len,
+                                  int32_t num_kv_heads, int32_t head_dim,
+                                  int32_t dtype);
+
+/* Same as dx_attn_prefill (bf16 only), with V already transposed: position
+ * p of sequence s, kv head g, dim d at vt[(g * head_dim + d) * vt_ld +
+ * vt_start[s] + p]. This is the layout dx_transpose_v writes; the model
+ * driver produces it once per layer. Each vt_start[s] is a multiple of 8 and
+ * columns [vt_start[s], vt_start[s] + seq_len[s] rounded up to 64) lie inside
+ * vt_ld and hold zeros past seq_len[s] (dx_transpose_v writes them). */
+int dx_attn_prefill_vt(const void *q, const void *k, const void *vt, void *out,
+                       const int32_t *seq_start, const int32_t *seq_len,
+                       const int32_t *vt_start, int32_t num_seqs,
+                       int32_t max_seq_len,
+                       int32_t num_q_heads, int32_t num_kv_heads,
+                       int32_t head_dim, int64_t q_row_stride,
+                       int64_t k_row_stride, int64_t vt_ld,
+                       int64_t out_row_stride, float scale, float softcap,
+                       int32_t window, int32_t causal, void *stream);
+
+/* V of every sequence (rows seq_start[s] + p, kv head g at g * head_dim) into
+ * vt[(g * head_dim + d) * vt_ld + vt_start[s] + p] (bf16), writing zeros for
+ * p in [seq_len[s], seq_len[s] rounded up to 64). head_dim % 64 == 0. Layout
+ * helper for dx_attn_prefill_vt; no reference counterpart (the reference
+ * repeats K/V to every query head instead, blocked.py:12-13). */
+int dx_transpose_v(const void *v, void *vt, const int32_t *seq_start,
+                   const int32_t *seq_len, const int32_t *vt_start,
+                   int32_t num_seqs, int32_t max_seq_len, int32_t num_kv_heads,
+                   int32_t head_dim, int64_t v_row_stride, int64_t vt_ld,
+                   void *stream);
+
+/* ------------------------------------------------------------------------ */
+/* Projections and MLP                                                       */
+/* ------------------------------------------------------------------------ */
+
+/* y[m, n] = x[m, k] @ w[n, k]^T with bf16 operands and fp32 accumulation;
+ * y is bf16 (rounded once) or fp32. Replaces `linear` in src/deciax/nn.py:11-19
+ * (PyTorch [out, in] weight layout, fp32 accumulation) followed by the
+ * `.astype(x.dtype)` of `dense`, src/deciax/models/qwen3_5/text.py:21-22.
+ * Requires n % 256 == 0, k % 64 == 0, 16-byte aligned rows. */
+int dx_linear(const void *x, const void *w, void *y, int64_t m, int64_t n,
+              int64_t k, int64_t ldx, int64_t ldw, int64_t ldy,
+              int32_t out_dtype, void *stream);
+
+/* Gated projection: for a packed gate|up weight (dx_pack_gate_up layout,
+ * [2f, k]), act[m, f] = bf16(bf16(act(bf16(x @ gate^T))) * bf16(x @ up^T)).
+ * The rounding points are those of src/deciax/kernels/swiglu.py:100-101
+ * (`gu.astype(bf16)`, activation, product rounded to bf16). Requires
+ * f % 128 == 0, k % 64 == 0. */
+int dx_gated_linear(const void *x, const void *gate_up, void *act, int64_t m,
+                    int64_t f, int64_t k, int64_t ldx, int64_t ld_act,
+                    int32_t activation, void *stream);
+
+/* Pack gate[f, k] and up[f, k] (PyTorch layout) into the [2f, k] layout of
+ * dx_gated_linear: rows [128 b, 128 b + 64) are gate rows [64 b, 64 b + 64)
+ * and rows [128 b + 64, 128 b + 128) are the matching up rows. Replaces `pack`
+ * in src/deciax/kernels/swiglu.py:45-51 (gate|up per intermediate tile). */
+int dx_pack_gate_up(const void *gate, const void *up, void *packed, int64_t f,
+                    int64_t k, void *stream);
+
+/* Fused RMSNorm + packed projection: h = bf16(x * rsqrt(mean(x^2) + eps) * (1 + norm_w)),
+ * optionally h *= row_mask (uint8, nullable), y[rows, n] = bf16(h @ w[n, d]^T).
+ * Replaces `norm_project` in src/deciax/kernels/projection.py:13-53 (the
+ * packed weight is [n, d] here, K-contiguous for the MFMA operand loads).
+ * Workspace holds h; size from dx_norm_project_workspace. */
+int dx_norm_project(const void *x, const void *norm_w, const uint8_t *row_mask,
+                    const void *w, void *y, int64_t rows, int64_t d, int64_t n,
+                    float eps, void *workspace, int64_t workspace_bytes,
+                    void *stream);
+
+int64_t dx_norm_project_workspace(int64_t rows, int64_t d);
+
+/* Fused RMSNorm + gated MLP: h = rms(x)(1 + norm_w) in bf16, a = gated(h), y =
+ * a @ down[d, f]^T with fp32 accumulation over all of f; y is fp32 (the
+ * partial the reference reduces across shards) or bf16. Replaces
+ * `fused_mlp_partial` in src/deciax/kernels/swiglu.py:166-208. gate_up is the
+ * dx_pack_gate_up layout; down is [d, f] (PyTorch layout). */
+int dx_mlp(const void *x, const void *norm_w, const void *gate_up,
+           const void *down, void *y, int64_t rows, int64_t d, int64_t f,
+           float eps, int32_t activation, int32_t out_dtype, void *workspace,
+           int64_t workspace_bytes, void *stream);
+
+int64_t dx_mlp_workspace(int64_t rows, int64_t d, int64_t f);
+
+/* ------------------------------------------------------------------------ */
+/* Norms, embedding, RoPE                                                    */
+/* ------------------------------------------------------------------------ */
+
+/* y = bf16(x * rsqrt(mean(x^2) + eps) * (1 + w)) per row, fp32 inside.
+ * Replaces `rms` in src/deciax/models/qwen3_5/text.py:25-28. */
+int dx_rmsnorm(const void *x, const void *w, void *y, int64_t rows, int64_t d,
+               int64_t ldx, int64_t ldy, float eps, void *stream);
+
+/* Residual update of one layer half, in place on x:
+ *   t = post_w ? bf16(rms(y) * (1 + post_w)) : y;   x = bf16(x + t);
+ *   if h: h = bf16(rms(x) * (1 + next_w)).
+ * With post_w == NULL this is the pre-norm residual of
+ * src/deciax/models/qwen3_5/text.py:96-102 (`x + attn`, then the next rms);
+ * with post_w it is the Gemma-2 sandwich (post-norm before the add). */
+int dx_add_rmsnorm(const void *y, const void *post_w, void *x,
+                   const void *next_w, void *h, int64_t rows, int64_t d,
+                   float eps, void *stream);
+
+/* x[t] = bf16(table[ids[t]] * scale) for t < tokens (scale is applied to the
+ * bf16 value; pass 1 for a plain gather); if h: h = bf16(rms(x) * (1 + norm_w)).
+ * Replaces `_embed` in src/deciax/models/clef/model.py:81,95. Ids outside
+ * [0, vocab) are clamped into range by the kernel; the Python layer rejects
+ * them before the call. */
+int dx_embed(const int32_t *ids, const void *table, void *x, int64_t tokens,
+             int64_t d, int64_t vocab, float scale, const void *norm_w,
+             void *h, float eps, void *stream);
+
+/* In-place rotate-half RoPE on heads [0, num_heads) of each row:
+ * x[j] <- bf16(bf16(x[j] cos[p, j']) + bf16(rot(x)[j] sin[p, j'])), j' = j mod D/2,
+ * rot(x)[j] = -x[j + D/2] (j < D/2), x[j - D/2] (j >= D/2), p = positions[row].
+ * cos/sin are bf16 tables [max_pos, D/2]. Replaces `apply_rope` in
+ * src/deciax/nn.py:35-44 (positions are per row, so packed sequences restart
+ * at 0). */
+int dx_rope(void *x, const int32_t *positions, const void *cos,
+            const void *sin, int64_t rows, int32_t num_heads, int32_t head_dim,
+            int64_t row_stride, int32_t max_pos, void *stream);
+
+/* ------------------------------------------------------------------------ */
+/* Option readout                                                            */
+/* ------------------------------------------------------------------------ */
+
+/* For option o (question q owns options [q_offsets[q], q_offsets[q + 1])):
+ *   g = bf16(rms(hidden[opt_pos[o]]) * (1 + norm_w))
+ *   z = <g, table[opt_label[o]]>            (fp32 accumulation)
+ *   logits[o] = softcap > 0 ? softcap * tanh(z / softcap) : z
+ *   probs[o]  = softmax over the options of its question (fp32).
+ * Positions are clamped into [0, hidden_rows) and labels into [0, vocab) by
+ * the kernel; callers validate them first.
+ * Replaces the marker gather + score + per-question softmax of `_scorer`,
+ * src/deciax/models/laya/heads.py:74-91 (gather at marker_pos, masked
+ * softmax) and the softmax of `decode`, src/deciax/models/clef/input.py:185-194
+ * (per-field softmax of the option logits). */
+int dx_readout(const void *hidden, const void *norm_w, const void *table,
+               const int32_t *opt_pos, const int32_t *opt_label,
+               const int32_t *q_offsets, int32_t num_questions,
+               int64_t num_options, int64_t hidden_rows, int64_t d,
+               int64_t ld_hidden, int64_t vocab, float eps, float softcap,
+               float *logits, float *probs, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DECIAX_HIP_H */

@@ -1,0 +1,96 @@
+"""Causal GQA prefill attention, restated in numpy (test infrastructure only).
+
+Follows `attention` in src/deciax/kernels/attention/blocked.py:9-32: K/V
+repeated to every query head (:12-13), queries in blocks of 128 (:15-17),
+fp32 scores times the scale (:21), masked scores set to MASK_FILL = -1e30
+(src/deciax/kernels/attention/reference.py:8, blocked.py:23-27), softmax in
+fp32, weights rounded to the input dtype (:27), P.V accumulated in fp32 and
+rounded (:28-29).
+
+Gemma-2 additions the reference has no code for:
+  * logit soft-capping after scaling and before the mask,
+    TF/models/gemma2/modeling_gemma2.py:203-211;
+  * the causal sliding window `q - W < k <= q`, TF/masking_utils.py:92-99,134-138
+    (the reference's own window is symmetric, reference.py:14-16, and is what
+    `causal=False` with a window gives here).
+"""
+
+from __future__ import annotations
+
+from collections.abc import Sequence
+
+import numpy as np
+
+from oracle.numerics import F32, maybe, softcap
+
+MASK_FILL = F32(-1e30)
+BLOCK = 128
+
+
+def visible(qpos: np.ndarray, kpos: np.ndarray, length: int, window: int, causal: bool) -> np.ndarray:
+    """[nq, nk] boolean: may query qpos[i] attend to key kpos[j]."""
+    qp = np.asarray(qpos)[:, None]
+    kp = np.asarray(kpos)[None, :]
+    ok = kp < length
+    if causal:
+        ok = ok & (kp <= qp)
+        if window > 0:
+            ok = ok & (kp > qp - window)
+    elif window > 0:
+        ok = ok & (np.abs(qp - kp) <= window)
+    return ok
+
+
+def attention_seq(q: np.ndarray, k: np.ndarray, v: np.ndarray, *, scale: float, softcap_value: float = 0.0,
+                  window: int = 0, causal: bool = True, bf16: bool = True,
+                  query_pos: Sequence[int] | None = None) -> np.ndarray:
+    """One sequence: q [L, Hq, D], k/v [L, Hkv, D] (values already in the input dtype) ->
+    out [nq, Hq, D] for the query positions `query_pos` (default: all L)."""
+    length, hq, d = q.shape
+    hkv = k.shape[1]
+    group = hq // hkv
+    qpos = np.arange(length) if query_pos is None else np.asarray(query_pos)
+    out = np.zeros((len(qpos), hq, d), F32)
+    kpos = np.arange(length)
+    for b0 in range(0, len(qpos), BLOCK):
+        rows = qpos[b0:b0 + BLOCK]
+        ok = visible(rows, kpos, length, window, causal)
+        for h in range(hq):
+            g = h // group
+            scores = (q[rows, h, :].astype(F32) @ k[:, g, :].astype(F32).T).astype(F32) * F32(scale)
+            scores = softcap(scores, softcap_value)
+            scores = np.where(ok, scores, MASK_FILL)
+            m = scores.max(axis=1, keepdims=True)
+            e = np.exp(scores - m)
+            w = (e / e.sum(axis=1, keepdims=True)).astype(F32)
+            w = maybe(w, bf16)
+            out[b0:b0 + len(rows), h, :] = maybe(w @ v[:, g, :].astype(F32), bf16)
+    return out
+
+
+def attention_packed(q: np.ndarray, k: np.ndarray, v: np.ndarray, seq_start: Sequence[int], seq_len: Sequence[int],
+                     *, scale: float, softcap_value: float = 0.0, window: int = 0, causal: bool = True,
+                     bf16: bool = True) -> np.ndarray:
+    """Packed rows: q [R, Hq, D], k/v [R, Hkv, D]; sequence s is rows [start_s, start_s + len_s).
+    Rows outside every sequence stay zero."""
+    out = np.zeros(q.shape, F32)
+    for start, length in zip(seq_start, seq_len):
+        sl = slice(start, start + length)
+        out[sl] = attention_seq(q[sl], k[sl], v[sl], scale=scale, softcap_value=softcap_value, window=window,
+                                causal=causal, bf16=bf16)
+    return out
+
+
+def attention_flops(lengths: Sequence[int], *, num_q_heads: int, head_dim: int, window: int = 0,
+                    causal: bool = True) -> int:
+    """4 * D * Hq * (number of visible (query, key) pairs): the algorithmic work of one layer."""
+    pairs = 0
+    for n in lengths:
+        if causal and window <= 0:
+            pairs += n * (n + 1) // 2
+        elif causal:
+            w = min(window, n)
+            pairs += w * (w + 1) // 2 + (n - w) * w
+        else:
+            pairs += n * n if window <= 0 else int(visible(np.arange(n), np.arange(n), n, window, False).sum())
+    return 4 * head_dim * num_q_heads * pairs

@@ -1,0 +1,69 @@
+"""bf16 rounding and the elementwise functions of the path (test infrastructure only)."""
+
+from __future__ import annotations
+
+import numpy as np
+
+F32 = np.float32
+
+
+def bf16(x: np.ndarray) -> np.ndarray:
+    """Round fp32 values to the nearest bf16 (ties to even); result kept as fp32.
+
+    This is the rounding of `astype(jnp.bfloat16)` in the reference (e.g.
+    src/deciax/kernels/swiglu.py:100-101) and of torch's `.to(torch.bfloat16)`."""
+    x = np.ascontiguousarray(x, dtype=F32)
+    u = x.view(np.uint32)
+    rounded = (u + (((u >> 16) & 1) + np.uint32(0x7FFF))) & np.uint32(0xFFFF0000)
+    out = rounded.view(F32).copy()
+    nan = np.isnan(x)
+    if nan.any():
+        out[nan] = np.nan
+    return out
+
+
+def bf16_bits(x: np.ndarray) -> np.ndarray:
+    """uint16 bit patterns of bf16(x)."""
+    return (bf16(x).view(np.uint32) >> 16).astype(np.uint16)
+
+
+def from_bits(bits: np.ndarray) -> np.ndarray:
+    """bf16 bit patterns -> fp32 values."""
+    return (np.asarray(bits, np.uint16).astype(np.uint32) << 16).view(F32)
+
+
+def maybe(x: np.ndarray, on: bool) -> np.ndarray:
+    return bf16(x) if on else np.asarray(x, F32)
+
+
+def gelu_tanh(x: np.ndarray) -> np.ndarray:
+    """0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))) — TF/activations.py:31-45
+    (`gelu_pytorch_tanh`, the Gemma-2 hidden activation)."""
+    x = np.asarray(x, F32)
+    inner = F32(0.7978845608028654) * (x + F32(0.044715) * x * x * x)
+    return (F32(0.5) * x * (F32(1.0) + np.tanh(inner))).astype(F32)
+
+
+def silu(x: np.ndarray) -> np.ndarray:
+    """x * sigmoid(x) — the reference's SwiGLU activation (src/deciax/kernels/swiglu.py:101)."""
+    x = np.asarray(x, F32)
+    return (x / (F32(1.0) + np.exp(-x))).astype(F32)
+
+
+ACTIVATIONS = {"gelu_tanh": gelu_tanh, "silu": silu}
+
+
+def softcap(x: np.ndarray, cap: float) -> np.ndarray:
+    """cap * tanh(x / cap) — TF/models/gemma2/modeling_gemma2.py:203-206 (attention) and
+    :527-530 (final logits); identity for cap <= 0."""
+    if cap <= 0:
+        return np.asarray(x, F32)
+    c = F32(cap)
+    return (c * np.tanh(np.asarray(x, F32) / c)).astype(F32)
+
+
+def softmax(z: np.ndarray) -> np.ndarray:
+    """max-subtracted softmax in fp32 — src/deciax/protocol/answers.py:44-46."""
+    z = np.asarray(z, F32)
+    e = np.exp(z - z.max())
+    return (e / e.sum()).astype(F32)

@@ -1,0 +1,428 @@
+"""Kernel parity on the GPU: each C-ABI entry point against the oracle on seeded inputs.
+
+Tolerances: bf16 results within 2e-2 relative (the reference's bf16 kernel
+tests use 2e-2, tests/kernels/test_attention.py:54-62 and test_fused.py:80-90);
+fp32 attention within 1e-4; GEMMs within one bf16 rounding step; integer /
+gather outputs exact.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from tests.conftest import bf16_np, i32, rng, say, to_dev, to_np
+
+pytestmark = pytest.mark.gpu
+
+
+def close(got: np.ndarray, want: np.ndarray, rel: float) -> None:
+    """max |got - want| <= rel * max |want|, and elementwise within rel (+ rel * rms(want))."""
+    got, want = np.asarray(got, np.float64), np.asarray(want, np.float64)
+    assert np.isfinite(got).all(), "non-finite output"
+    scale = float(np.abs(want).max()) or 1.0
+    err = float(np.abs(got - want).max())
+    assert err <= rel * scale, f"max abs error {err:.3e} > {rel} * {scale:.3e}"
+    rms = float(np.sqrt(np.mean(want * want))) or 1.0
+    np.testing.assert_allclose(got, want, rtol=rel, atol=rel * rms)
+
+
+# ----------------------------------------------------------------------------- GEMMs
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 256, 64), (100, 512, 128), (1024, 256, 320), (1500, 768, 512),
+                                   (4096, 1024, 3584)])
+def test_linear_bf16(m: int, n: int, k: int) -> None:
+    from deciax_amd import kernels as K
+    from oracle.model import linear
+
+    say(f"linear bf16 m={m} n={n} k={k}")
+    r = rng(m + n + k)
+    x, w = bf16_np(r.normal(size=(m, k))), bf16_np(r.normal(size=(n, k)) * 0.05)
+    got = to_np(K.linear(to_dev(x), to_dev(w)))
+    want = linear(x, w)
+    # identical up to fp32 summation order: at most one bf16 step apart
+    np.testing.assert_allclose(got, want, rtol=2 ** -7, atol=1e-6)
+    assert (got == want).mean() > 0.95
+
+
+def test_linear_f32_and_strides() -> None:
+    import torch
+
+    from deciax_amd import kernels as K
+
+    say("linear fp32 with strided input view")
+    r = rng(7)
+    x = bf16_np(r.normal(size=(300, 512)))
+    w = bf16_np(r.normal(size=(256, 256)))
+    xd = to_dev(x)[:, 128:384]  # row stride 512, k = 256
+    got = to_np(K.linear(xd, to_dev(w), out_dtype=torch.float32))
+    want = x[:, 128:384].astype(np.float64) @ w.T.astype(np.float64)
+    np.testing.assert_allclose(got, want, rtol=1e-5, atol=1e-4)
+
+
+@pytest.mark.parametrize("act", ["gelu_tanh", "silu"])
+@pytest.mark.parametrize("m", [7, 513, 2048])
+def test_gated_linear(act: str, m: int) -> None:
+    from deciax_amd import kernels as K
+    from oracle.model import gated
+
+    say(f"gated_linear {act} m={m}")
+    r = rng(m)
+    k, f = 256, 384
+    x = bf16_np(r.normal(size=(m, k)))
+    gate, up = (bf16_np(r.normal(size=(f, k)) * 0.1) for _ in range(2))
+    packed = K.pack_gate_up(to_dev(gate), to_dev(up))
+    got = to_np(K.gated_linear(to_dev(x), packed, act))
+    want = gated(x, gate, up, act)
+    close(got, want, 2e-2)
+    assert (np.abs(got - want) <= np.abs(want) * 2 ** -7 + 1e-6).mean() > 0.97
+
+
+def test_pack_gate_up_layout() -> None:
+    from deciax_amd import kernels as K
+
+    say("pack_gate_up layout")
+    f, k = 256, 64
+    gate = np.arange(f * k, dtype=np.float32).reshape(f, k) % 251
+    up = -gate
+    got = to_np(K.pack_gate_up(to_dev(gate), to_dev(up)))
+    for blk in range(f // 64):
+        np.testing.assert_array_equal(got[128 * blk:128 * blk + 64], bf16_np(gate[64 * blk:64 * blk + 64]))
+        np.testing.assert_array_equal(got[128 * blk + 64:128 * blk + 128], bf16_np(up[64 * blk:64 * blk + 64]))
+
+
+def test_mlp_small() -> None:
+    import torch
+
+    from deciax_amd import kernels as K
+    from oracle.model import mlp
+
+    say("mlp rows=600 d=512 f=1024")
+    r = rng(3)
+    rows, d, f = 600, 512, 1024
+    x = bf16_np(r.normal(size=(rows, d)))
+    norm = bf16_np(r.normal(size=d) * 0.02)
+    gate, up = (bf16_np(r.normal(size=(f, d)) * 0.02) for _ in range(2))
+    down = bf16_np(r.normal(size=(d, f)) * 0.02)
+    packed = K.pack_gate_up(to_dev(gate), to_dev(up))
+    got = to_np(K.mlp(to_dev(x), to_dev(norm), packed, to_dev(down), eps=1e-6, out_dtype=torch.float32))
+    want = mlp(x, norm, gate, up, down, eps=1e-6)
+    close(got, want, 2e-2)
+
+
+def test_mlp_full_shape_sampled_rows() -> None:
+    """The fused gated MLP at 8192 x 3584 x 14336; rows are independent, so the oracle checks a sample."""
+    import torch
+
+    from deciax_amd import kernels as K
+    from oracle.model import mlp
+
+    say("mlp full shape T=8192 H=3584 I=14336")
+    r = rng(0)
+    rows, d, f = 8192, 3584, 14336
+    x = bf16_np(r.normal(size=(rows, d)).astype(np.float32))
+    norm = bf16_np((r.normal(size=d) * 0.02).astype(np.float32))
+    gate = bf16_np((r.normal(size=(f, d)) * 0.02).astype(np.float32))
+    up = bf16_np((r.normal(size=(f, d)) * 0.02).astype(np.float32))
+    down = bf16_np((r.normal(size=(d, f)) * 0.02).astype(np.float32))
+    packed = K.pack_gate_up(to_dev(gate), to_dev(up))
+    y = K.mlp(to_dev(x), to_dev(norm), packed, to_dev(down), eps=1e-6, out_dtype=torch.bfloat16)
+    torch.cuda.synchronize()
+    sample = np.concatenate([[0, 1, rows - 1], r.choice(rows, 61, replace=False)])
+    got = to_np(y)[sample]
+    want = mlp(x[sample], norm, gate, up, down, eps=1e-6, round_out=True)
+    close(got, want, 2e-2)
+
+
+# ----------------------------------------------------------------------------- attention
+
+
+def _packed_case(seed: int, lengths: list[int], hq: int, hkv: int, d: int, dtype: str = "bf16",
+                 scale: float = 0.5):
+    r = rng(seed)
+    rows = int(sum(lengths))
+    q = r.normal(size=(rows, hq, d)).astype(np.float32) * scale
+    k = r.normal(size=(rows, hkv, d)).astype(np.float32) * scale
+    v = r.normal(size=(rows, hkv, d)).astype(np.float32) * scale
+    if dtype == "bf16":
+        q, k, v = bf16_np(q), bf16_np(k), bf16_np(v)
+    starts = np.concatenate([[0], np.cumsum(lengths)[:-1]]).astype(np.int64)
+    return q, k, v, starts
+
+
+ATTN_CASES = [
+    # (lengths, hq, hkv, d, window, softcap, causal)
+    ([139, 97], 4, 2, 128, 0, 0.0, True),
+    ([1, 63, 64, 65, 130], 4, 2, 128, 0, 50.0, True),
+    ([300, 257], 16, 8, 256, 64, 50.0, True),
+    ([513], 16, 8, 256, 0, 50.0, True),
+    ([200, 129], 8, 8, 64, 3, 0.0, True),
+    ([256, 100], 8, 2, 64, 0, 30.0, True),
+    ([256, 251], 4, 4, 64, 0, 0.0, False),
+    ([256, 219], 4, 4, 64, 64, 0.0, False),
+    ([700], 4, 2, 256, 128, 0.0, True),
+    ([64, 1, 2], 4, 1, 128, 0, 80.0, True),
+]
+
+
+@pytest.mark.parametrize("lengths,hq,hkv,d,window,softcap,causal", ATTN_CASES)
+def test_attention_bf16_packed(lengths, hq, hkv, d, window, softcap, causal) -> None:
+    from deciax_amd import kernels as K
+    from oracle.attention import attention_packed
+
+    say(f"attention bf16 lengths={lengths} hq={hq} hkv={hkv} d={d} window={window} softcap={softcap} causal={causal}")
+    q, k, v, starts = _packed_case(len(lengths) + d + window, lengths, hq, hkv, d)
+    rows = q.shape[0]
+    out = K.attention_varlen(to_dev(q.reshape(rows, -1)), to_dev(k.reshape(rows, -1)), to_dev(v.reshape(rows, -1)),
+                             i32(starts), i32(lengths), max(lengths), num_q_heads=hq, num_kv_heads=hkv, head_dim=d,
+                             scale=d ** -0.5, softcap=softcap, window=window, causal=causal)
+    got = to_np(out).reshape(rows, hq, d)
+    want = attention_packed(q, k, v, starts, lengths, scale=d ** -0.5, softcap_value=softcap, window=window,
+                            causal=causal)
+    close(got, want, 2e-2)
+
+
+def test_attention_vt_path_matches_generic() -> None:
+    """The model driver's form (V transposed once per layer into 64-aligned per-sequence blocks)."""
+    import torch
+
+    from deciax_amd import kernels as K
+
+    say("attention vt path vs generic")
+    lengths = [77, 300, 5]
+    hq, hkv, d = 16, 8, 256
+    q, k, v, starts = _packed_case(11, lengths, hq, hkv, d)
+    rows = q.shape[0]
+    qd, kd, vd = (to_dev(a.reshape(rows, -1)) for a in (q, k, v))
+    padded = [(n + 63) // 64 * 64 for n in lengths]
+    vt_start = np.concatenate([[0], np.cumsum(padded)[:-1]])
+    vt = torch.full((hkv * d, int(sum(padded))), float("nan"), dtype=torch.bfloat16, device="cuda")
+    K.transpose_v(vd, vt, i32(starts), i32(lengths), i32(vt_start), max(lengths), num_kv_heads=hkv, head_dim=d)
+    a = K.attention_vt(qd, kd, vt, i32(starts), i32(lengths), i32(vt_start), max(lengths), num_q_heads=hq,
+                       num_kv_heads=hkv, head_dim=d, scale=1 / 16, softcap=50.0, window=0)
+    b = K.attention_varlen(qd, kd, vd, i32(starts), i32(lengths), max(lengths), num_q_heads=hq, num_kv_heads=hkv,
+                           head_dim=d, scale=1 / 16, softcap=50.0, window=0)
+    np.testing.assert_array_equal(to_np(a), to_np(b))
+    # the transposed block holds V^T and zeros past each length
+    vt_np = to_np(vt)
+    for s, n, p0 in zip(starts, lengths, vt_start):
+        np.testing.assert_array_equal(vt_np[:, p0:p0 + n], v[s:s + n].reshape(n, -1).T)
+        assert (vt_np[:, p0 + n:p0 + (n + 63) // 64 * 64] == 0).all()
+
+
+def test_attention_fp32_config1() -> None:
+    """Single causal GQA prefill in fp32: B1 S512 8/4 heads x 128, q/k/v ~ N(0,1) from seed 0, 1e-4."""
+    from deciax_amd import kernels as K
+    from oracle.attention import attention_seq
+
+    say("attention fp32 B1 S512 8/4x128")
+    r = rng(0)
+    s, hq, hkv, d = 512, 8, 4, 128
+    q = r.normal(size=(1, s, hq, d)).astype(np.float32)
+    k = r.normal(size=(1, s, hkv, d)).astype(np.float32)
+    v = r.normal(size=(1, s, hkv, d)).astype(np.float32)
+    got = to_np(K.attention(to_dev(q, "f32"), to_dev(k, "f32"), to_dev(v, "f32"), to_dev(np.ones((1, s)), "f32"),
+                            causal=True))
+    want = attention_seq(q[0], k[0], v[0], scale=d ** -0.5, bf16=False)
+    np.testing.assert_allclose(got[0], want, rtol=1e-4, atol=1e-4)
+
+
+@pytest.mark.parametrize("window", [0, 64])
+def test_attention_fp32_window_softcap(window: int) -> None:
+    from deciax_amd import kernels as K
+    from oracle.attention import attention_packed
+
+    say(f"attention fp32 window={window}")
+    lengths = [130, 65]
+    q, k, v, starts = _packed_case(5, lengths, 4, 2, 64, dtype="f32", scale=1.0)
+    rows = q.shape[0]
+    out = K.attention_varlen(*(to_dev(a.reshape(rows, -1), "f32") for a in (q, k, v)), i32(starts), i32(lengths),
+                             max(lengths), num_q_heads=4, num_kv_heads=2, head_dim=64, scale=0.125, softcap=20.0,
+                             window=window)
+    want = attention_packed(q, k, v, starts, lengths, scale=0.125, softcap_value=20.0, window=window, bf16=False)
+    np.testing.assert_allclose(to_np(out).reshape(want.shape), want, rtol=1e-4, atol=1e-4)
+
+
+def test_attention_padded_mask_interface() -> None:
+    """[B, S, H, D] + right-padded key mask (the ops.attention / blocked.attention interface)."""
+    from deciax_amd import kernels as K
+    from oracle.attention import attention_seq
+
+    say("attention padded interface")
+    r = rng(3)
+    b, s, hq, hkv, d = 2, 139, 4, 2, 128
+    q = bf16_np(r.normal(size=(b, s, hq, d)))
+    k = bf16_np(r.normal(size=(b, s, hkv, d)))
+    v = bf16_np(r.normal(size=(b, s, hkv, d)))
+    mask = np.arange(s)[None] < np.array([s, 97])[:, None]
+    got = to_np(K.attention(to_dev(q), to_dev(k), to_dev(v), i32(mask.astype(np.int32)), causal=True))
+    for bi, n in enumerate((s, 97)):
+        want = attention_seq(q[bi, :n], k[bi, :n], v[bi, :n], scale=d ** -0.5)
+        close(got[bi, :n], want, 2e-2)
+        assert (got[bi, n:] == 0).all()
+    with pytest.raises(ValueError, match="prefix"):
+        bad = mask.copy()
+        bad[0, 5] = False
+        K.attention(to_dev(q), to_dev(k), to_dev(v), i32(bad.astype(np.int32)), causal=True)
+
+
+@pytest.mark.parametrize("window", [4096, 0, 512])
+def test_attention_layer_pair_full_shape(window: int) -> None:
+    """Gemma-2-9B attention layer at batch 8 x 2048, 16/8 heads x 256, softcap 50, scale 1/16: the
+    sliding layer (window 4096, inactive at 2048), the global layer, and a window-active variant.
+    Query rows are independent given K/V, so the oracle checks sampled rows of every head."""
+    import torch
+
+    from deciax_amd import kernels as K
+    from oracle.attention import attention_seq
+
+    say(f"attention full shape B8 S2048 16/8x256 window={window}")
+    r = rng(0)
+    b, s, hq, hkv, d = 8, 2048, 16, 8, 256
+    q = bf16_np(r.normal(size=(b * s, hq, d)).astype(np.float32) * 0.5)
+    k = bf16_np(r.normal(size=(b * s, hkv, d)).astype(np.float32) * 0.5)
+    v = bf16_np(r.normal(size=(b * s, hkv, d)).astype(np.float32) * 0.5)
+    starts = np.arange(b) * s
+    out = K.attention_varlen(to_dev(q.reshape(b * s, -1)), to_dev(k.reshape(b * s, -1)),
+                             to_dev(v.reshape(b * s, -1)), i32(starts), i32([s] * b), s, num_q_heads=hq,
+                             num_kv_heads=hkv, head_dim=d, scale=1 / 16, softcap=50.0, window=window)
+    torch.cuda.synchronize()
+    got = to_np(out).reshape(b, s, hq, d)
+    for bi in (0, b - 1):
+        rows = np.unique(np.concatenate([[0, 1, 63, 64, 1000, s - 1], r.choice(s, 10, replace=False)]))
+        sl = slice(bi * s, (bi + 1) * s)
+        want = attention_seq(q[sl], k[sl], v[sl], scale=1 / 16, softcap_value=50.0, window=window, query_pos=rows)
+        close(got[bi, rows], want, 2e-2)
+
+
+# ----------------------------------------------------------------------------- row kernels
+
+
+def test_rmsnorm_and_masked_norm_project() -> None:
+    from deciax_amd import kernels as K
+    from oracle.model import linear, rmsnorm
+
+    say("rmsnorm + norm_project")
+    r = rng(1)
+    x = bf16_np(r.normal(size=(333, 3584)) * 3)
+    w = bf16_np(r.normal(size=3584) * 0.1)
+    got = to_np(K.rmsnorm(to_dev(x), to_dev(w), eps=1e-6))
+    want = rmsnorm(x, w, 1e-6)
+    np.testing.assert_allclose(got, want, rtol=2 ** -7, atol=0)
+    assert (got == want).mean() > 0.99
+    wp = bf16_np(r.normal(size=(512, 3584)) * 0.02)
+    mask = r.random(333) > 0.3
+    y = to_np(K.norm_project(to_dev(x), to_dev(w), to_dev(wp), eps=1e-6, row_mask=i32(mask)))
+    want = linear(want * mask[:, None], wp)
+    close(y, want, 2e-2)
+    assert (y[~mask] == 0).all()
+
+
+@pytest.mark.parametrize("post,nxt", [(True, True), (True, False), (False, True), (False, False)])
+def test_add_rmsnorm(post: bool, nxt: bool) -> None:
+    from deciax_amd import kernels as K
+    from oracle.model import rmsnorm
+
+    say(f"add_rmsnorm post={post} next={nxt}")
+    r = rng(2)
+    rows, d = 257, 4608
+    y, x = bf16_np(r.normal(size=(rows, d))), bf16_np(r.normal(size=(rows, d)))
+    pw, nw = bf16_np(r.normal(size=d) * 0.1), bf16_np(r.normal(size=d) * 0.1)
+    xd = to_dev(x)
+    h = K.add_rmsnorm(to_dev(y), xd, eps=1e-6, post_w=to_dev(pw) if post else None,
+                      next_w=to_dev(nw) if nxt else None)
+    t = rmsnorm(y, pw, 1e-6) if post else y
+    x_want = bf16_np(x + t)
+    np.testing.assert_allclose(to_np(xd), x_want, rtol=2 ** -7, atol=0)
+    if nxt:
+        np.testing.assert_allclose(to_np(h), rmsnorm(x_want, nw, 1e-6), rtol=2 ** -7, atol=0)
+    else:
+        assert h is None
+
+
+def test_embed_scale_and_first_norm() -> None:
+    from deciax_amd import gemma
+    from deciax_amd import kernels as K
+    from oracle.model import embed_scale, rmsnorm
+
+    say("embed")
+    r = rng(4)
+    vocab, d = 1000, 3584
+    table = bf16_np(r.normal(size=(vocab, d)) * 0.02)
+    ids = r.integers(0, vocab, 77)
+    nw = bf16_np(r.normal(size=d) * 0.1)
+    scale = gemma.embed_scale(d)
+    assert scale == embed_scale(d)
+    x, h = K.embed(i32(ids), to_dev(table), scale=scale, norm_w=to_dev(nw), eps=1e-6)
+    x_want = bf16_np(table[ids] * np.float32(scale))
+    np.testing.assert_array_equal(to_np(x), x_want)
+    np.testing.assert_allclose(to_np(h), rmsnorm(x_want, nw, 1e-6), rtol=2 ** -7, atol=0)
+
+
+@pytest.mark.parametrize("d", [128, 256])
+def test_rope(d: int) -> None:
+    from deciax_amd import gemma
+    from deciax_amd import kernels as K
+    from oracle.model import rope, rope_tables
+
+    say(f"rope d={d}")
+    r = rng(d)
+    rows, heads = 300, 6
+    x = bf16_np(r.normal(size=(rows, heads * d + 64)))
+    pos = r.integers(0, 16384, rows)
+    cos_b, sin_b = gemma.rope_tables(16384, d, 10000.0)
+    cos_o, sin_o = rope_tables(16384, d, 10000.0)
+    from oracle.numerics import from_bits
+
+    np.testing.assert_array_equal(from_bits(cos_b), cos_o)
+    np.testing.assert_array_equal(from_bits(sin_b), sin_o)
+    xd = to_dev(x)
+    K.rope(xd, i32(pos), to_dev(cos_o), to_dev(sin_o), num_heads=heads, head_dim=d)
+    got = to_np(xd)
+    want = rope(x[:, :heads * d].reshape(rows, heads, d), pos, cos_o, sin_o).reshape(rows, -1)
+    np.testing.assert_array_equal(got[:, :heads * d], want)
+    np.testing.assert_array_equal(got[:, heads * d:], x[:, heads * d:])
+
+
+def test_readout() -> None:
+    from deciax_amd import kernels as K
+    from oracle.model import readout
+
+    say("readout")
+    r = rng(9)
+    rows, d, vocab = 500, 3584, 3000
+    hidden = bf16_np(r.normal(size=(rows, d)) * 4)
+    table = bf16_np(r.normal(size=(vocab, d)) * 0.02)
+    nw = bf16_np(r.normal(size=d) * 0.1)
+    counts = [2, 8, 3, 1, 5, 300]
+    q_off = np.concatenate([[0], np.cumsum(counts)])
+    n = int(q_off[-1])
+    pos = r.integers(0, rows, n)
+    lab = r.integers(0, vocab, n)
+    logits, probs = K.readout(to_dev(hidden), to_dev(nw), to_dev(table), i32(pos), i32(lab), i32(q_off), eps=1e-6,
+                              softcap=30.0)
+    z, p = readout(hidden, nw, table, pos, lab, q_off, eps=1e-6, cap=30.0)
+    np.testing.assert_allclose(to_np(logits), z, rtol=1e-4, atol=1e-4)
+    np.testing.assert_allclose(to_np(probs), p, rtol=1e-4, atol=1e-6)
+    for a, b in zip(q_off[:-1], q_off[1:]):
+        assert abs(to_np(probs)[a:b].sum() - 1) < 1e-5
+
+
+def test_abi_rejects_bad_arguments() -> None:
+    import torch
+
+    from deciax_amd import kernels as K
+
+    say("abi argument validation")
+    x = torch.zeros((16, 96), dtype=torch.bfloat16, device="cuda")
+    w = torch.zeros((256, 96), dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(ValueError, match="multiple of 64"):
+        K.linear(x, w)
+    q = torch.zeros((8, 4 * 96), dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(ValueError, match="head_dim"):
+        K.attention_varlen(q, q, q, i32([0]), i32([8]), 8, num_q_heads=4, num_kv_heads=4, head_dim=96, scale=1.0)
+    q = torch.zeros((8, 8 * 64), dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(ValueError, match="GQA group"):
+        K.attention_varlen(q, q[:, :64], q[:, :64], i32([0]), i32([8]), 8, num_q_heads=8, num_kv_heads=1,
+                           head_dim=64, scale=1.0)
