@@ -270,15 +270,14 @@ attn_bf16_kernel(const uint16_t *__restrict__ Q, const uint16_t *__restrict__ K,
 
   lsum += __shfl_xor(lsum, 32, 64);
   if (qi < len) {
-    const float inv = 1.f / lsum;
     uint16_t *op = O + (start + qi) * o_stride + (long)h * D + lhalf * 4;
 #pragma unroll
     for (int db = 0; db < NDB; ++db)
 #pragma unroll
       for (int grp = 0; grp < 4; ++grp) {
         u32x2 w;
-        w[0] = pack_bf2(o[db][grp * 4 + 0] * inv, o[db][grp * 4 + 1] * inv);
-        w[1] = pack_bf2(o[db][grp * 4 + 2] * inv, o[db][grp * 4 + 3] * inv);
+        w[0] = pack_bf2(o[db][grp * 4 + 0] / lsum, o[db][grp * 4 + 1] / lsum);
+        w[1] = pack_bf2(o[db][grp * 4 + 2] / lsum, o[db][grp * 4 + 3] / lsum);
         *reinterpret_cast<u32x2 *>(op + db * 32 + grp * 8) = w;
       }
   }
@@ -367,9 +366,8 @@ attn_f32_kernel(const float *__restrict__ Q, const float *__restrict__ K, const 
   }
   if (qi < len) {
     float *op = O + (start + qi) * o_stride + (long)h * D + part * DPT;
-    const float inv = 1.f / l;
 #pragma unroll
-    for (int d = 0; d < DPT; ++d) op[d] = o[d] * inv;
+    for (int d = 0; d < DPT; ++d) op[d] = o[d] / l;
   }
 }
 

@@ -7,6 +7,18 @@ fp32 scores times the scale (:21), masked scores set to MASK_FILL = -1e30
 fp32, weights rounded to the input dtype (:27), P.V accumulated in fp32 and
 rounded (:28-29).
 
+bf16 rounding of the probabilities has two forms in the reference:
+  * "normalized" — blocked.py:27-29 rounds the normalised softmax weights;
+  * "flash" (default) — the online-softmax kernel, pallas.py:104-116, rounds
+    the unnormalised p = exp(s - m) to the value dtype for P.V (pv_t, :47-49),
+    sums l from the unrounded p and divides at the end (:113-116).
+The two differ by bf16 noise (about 2^-9 relative per weight), which after a
+few layers is of the order of 1e-3 in option probabilities, so the oracle
+restates the flash form exactly as the GPU path evaluates it: the reference
+point m is the row maximum, except for soft-capped scores, where every score
+lies in (-cap, cap) and m is the fixed bound cap / 2 (the kernel needs no
+running max then). In fp32 the two forms coincide up to fp32 rounding.
+
 Gemma-2 additions the reference has no code for:
   * logit soft-capping after scaling and before the mask,
     TF/models/gemma2/modeling_gemma2.py:203-211;
@@ -21,7 +33,7 @@ from collections.abc import Sequence
 
 import numpy as np
 
-from oracle.numerics import F32, maybe, softcap
+from oracle.numerics import F32, acc_dtype, matmul, maybe, softcap
 
 MASK_FILL = F32(-1e30)
 BLOCK = 128
@@ -41,30 +53,42 @@ def visible(qpos: np.ndarray, kpos: np.ndarray, length: int, window: int, causal
     return ok
 
 
+FIXED_SHIFT_MAX_CAP = 56.0  # p = exp(t - cap/2) stays a normal fp32 / bf16 number for cap <= 56
+
+
 def attention_seq(q: np.ndarray, k: np.ndarray, v: np.ndarray, *, scale: float, softcap_value: float = 0.0,
                   window: int = 0, causal: bool = True, bf16: bool = True,
-                  query_pos: Sequence[int] | None = None) -> np.ndarray:
+                  query_pos: Sequence[int] | None = None, rounding: str = "flash") -> np.ndarray:
     """One sequence: q [L, Hq, D], k/v [L, Hkv, D] (values already in the input dtype) ->
     out [nq, Hq, D] for the query positions `query_pos` (default: all L)."""
+    if rounding not in ("flash", "normalized"):
+        raise ValueError(f"rounding must be 'flash' or 'normalized', got {rounding!r}")
     length, hq, d = q.shape
     hkv = k.shape[1]
     group = hq // hkv
     qpos = np.arange(length) if query_pos is None else np.asarray(query_pos)
     out = np.zeros((len(qpos), hq, d), F32)
     kpos = np.arange(length)
+    fixed = 0.0 < softcap_value <= FIXED_SHIFT_MAX_CAP
     for b0 in range(0, len(qpos), BLOCK):
         rows = qpos[b0:b0 + BLOCK]
         ok = visible(rows, kpos, length, window, causal)
         for h in range(hq):
             g = h // group
-            scores = (q[rows, h, :].astype(F32) @ k[:, g, :].astype(F32).T).astype(F32) * F32(scale)
+            scores = matmul(q[rows, h, :], k[:, g, :].T) * F32(scale)
             scores = softcap(scores, softcap_value)
             scores = np.where(ok, scores, MASK_FILL)
-            m = scores.max(axis=1, keepdims=True)
-            e = np.exp(scores - m)
-            w = (e / e.sum(axis=1, keepdims=True)).astype(F32)
-            w = maybe(w, bf16)
-            out[b0:b0 + len(rows), h, :] = maybe(w @ v[:, g, :].astype(F32), bf16)
+            vg = v[:, g, :].astype(F32)
+            if rounding == "normalized":
+                m = scores.max(axis=1, keepdims=True)
+                e = np.exp(scores - m)
+                w = maybe((e / e.sum(axis=1, keepdims=True)).astype(F32), bf16)
+                res = matmul(w, vg)
+            else:
+                m = F32(0.5 * softcap_value) if fixed else scores.max(axis=1, keepdims=True)
+                p = np.where(ok, np.exp(scores - m), F32(0.0)).astype(F32)
+                res = matmul(maybe(p, bf16), vg) / p.sum(axis=1, keepdims=True, dtype=acc_dtype()).astype(F32)
+            out[b0:b0 + len(rows), h, :] = maybe(res.astype(F32), bf16)
     return out
 
 

@@ -25,7 +25,7 @@ from dataclasses import dataclass
 import numpy as np
 
 from oracle.attention import attention_seq
-from oracle.numerics import ACTIVATIONS, F32, maybe, softcap, softmax
+from oracle.numerics import ACTIVATIONS, F32, matmul, maybe, softcap, softmax
 
 
 @dataclass(frozen=True)
@@ -59,7 +59,7 @@ def rmsnorm(x: np.ndarray, w: np.ndarray, eps: float, bf16: bool = True) -> np.n
 
 def linear(x: np.ndarray, w: np.ndarray, bf16: bool = True) -> np.ndarray:
     """x @ w.T, fp32 accumulation, one rounding — src/deciax/nn.py:11-19 + text.py:21-22."""
-    return maybe(np.asarray(x, F32) @ np.asarray(w, F32).T, bf16)
+    return maybe(matmul(x, np.asarray(w, F32).T), bf16)
 
 
 def gated(x: np.ndarray, gate: np.ndarray, up: np.ndarray, activation: str = "gelu_tanh",
@@ -75,8 +75,7 @@ def mlp(x: np.ndarray, norm_w: np.ndarray, gate: np.ndarray, up: np.ndarray, dow
     """RMSNorm -> gated -> down, fp32 accumulation over all of f
     (`fused_mlp_partial`, src/deciax/kernels/swiglu.py:166-208; fp32 out unless round_out)."""
     a = gated(rmsnorm(x, norm_w, eps, bf16), gate, up, activation, bf16)
-    y = np.asarray(a, F32) @ np.asarray(down, F32).T
-    return maybe(y, round_out and bf16)
+    return maybe(matmul(a, np.asarray(down, F32).T), round_out and bf16)
 
 
 def rope_tables(max_pos: int, head_dim: int, theta: float, bf16: bool = True) -> tuple[np.ndarray, np.ndarray]:

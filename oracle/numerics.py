@@ -2,9 +2,35 @@
 
 from __future__ import annotations
 
+from collections.abc import Iterator
+from contextlib import contextmanager
+
 import numpy as np
 
 F32 = np.float32
+_ACC = [np.dtype(np.float32)]
+
+
+def acc_dtype() -> np.dtype:
+    """Accumulation dtype of the oracle's contractions (fp32 unless inside `accumulation`)."""
+    return _ACC[-1]
+
+
+@contextmanager
+def accumulation(dtype: type) -> Iterator[None]:
+    """Run the oracle's matrix products in `dtype` (np.float64 gives the exactly-summed value of
+    every contraction, up to the bf16 rounding points, to measure fp32 summation-order noise)."""
+    _ACC.append(np.dtype(dtype))
+    try:
+        yield
+    finally:
+        _ACC.pop()
+
+
+def matmul(a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    """a @ b accumulated in `acc_dtype()`, returned as fp32."""
+    d = acc_dtype()
+    return (np.asarray(a, d) @ np.asarray(b, d)).astype(F32)
 
 
 def bf16(x: np.ndarray) -> np.ndarray:
