@@ -91,7 +91,7 @@ def validate_questions(questions: Mapping[Any, Any]) -> None:
     for qid, q in questions.items():
         if not isinstance(qid, str) or not qid:
             raise ValueError("question ids must be nonempty strings")
-        if not isinstance(q, Mapping) or q.get("type") not in QTYPES:
+        if not isinstance(q, Mapping) or not isinstance(q.get("type"), str) or q["type"] not in QTYPES:
             raise ValueError(f"{qid}: type must be noul, choice, or score")
         if any(k in q for k in ("labels", "option_order")):
             raise ValueError(f"{qid}: labels and option_order are not supported")

@@ -1,0 +1,255 @@
+"""Host logic on the CPU: the C-ABI library's exports, impl resolution and error mapping, schema
+encode/decode (the reference's tests/clef/test_input.py cases restated for this readout), and
+varlen batch packing. Nothing here launches a kernel."""
+
+from __future__ import annotations
+
+import ctypes
+from typing import Any
+
+import numpy as np
+import pytest
+
+from tests.conftest import rng
+
+
+# ----------------------------------------------------------------------------- C ABI
+
+
+def test_library_exports_every_header_symbol() -> None:
+    from deciax_amd import _lib
+
+    names = _lib.header_symbols()
+    assert len(names) >= 18, names
+    handle = _lib.lib()
+    missing = [n for n in names if not hasattr(handle, n)]
+    assert not missing, missing
+    assert set(names) == set(_lib.SIGNATURES), "every declared entry point has a ctypes signature"
+    assert handle.dx_version().decode().startswith("deciax-mi355x")
+
+
+def test_workspace_queries_are_host_arithmetic() -> None:
+    from deciax_amd import _lib
+
+    lib = _lib.lib()
+    # one 64-aligned V^T column block per sequence and kv head
+    assert lib.dx_attn_prefill_workspace(3, 100, 2, 128, _lib.DX_BF16) == 128 * 3 * 2 * 128 * 2
+    assert lib.dx_attn_prefill_workspace(3, 100, 2, 128, _lib.DX_F32) == 0
+    assert lib.dx_norm_project_workspace(10, 512) == 10 * 512 * 2 + (-(10 * 512 * 2)) % 256
+    assert lib.dx_mlp_workspace(8, 256, 512) >= 8 * 256 * 2 + 8 * 512 * 2
+
+
+def test_status_codes_map_to_reference_exceptions(monkeypatch: pytest.MonkeyPatch) -> None:
+    from deciax_amd import _lib
+
+    class FakeLib:
+        @staticmethod
+        def dx_last_error() -> bytes:
+            return b"boom"
+
+    monkeypatch.setattr(_lib, "lib", lambda: FakeLib)
+    _lib.check(_lib.DX_OK, "x")
+    for code in (_lib.DX_ERR_INVALID, _lib.DX_ERR_UNSUPPORTED):
+        with pytest.raises(ValueError, match="x: boom"):
+            _lib.check(code, "x")
+    with pytest.raises(RuntimeError, match="x: boom"):
+        _lib.check(_lib.DX_ERR_RUNTIME, "x")
+
+
+def test_header_constants_match_binding() -> None:
+    from deciax_amd import _lib
+
+    text = _lib.HEADER.read_text()
+    for name in ("DX_OK", "DX_ERR_INVALID", "DX_ERR_UNSUPPORTED", "DX_ERR_RUNTIME", "DX_BF16", "DX_F32",
+                 "DX_ACT_GELU_TANH", "DX_ACT_SILU"):
+        assert f"{name} = {getattr(_lib, name)}" in text, name
+
+
+def test_product_package_never_touches_the_oracle() -> None:
+    """The product path has no CPU fallback: no module of deciax_amd imports the oracle."""
+    import ast
+    from pathlib import Path
+
+    import deciax_amd
+
+    for path in Path(deciax_amd.__file__).parent.rglob("*.py"):
+        tree = ast.parse(path.read_text())
+        for node in ast.walk(tree):
+            names = []
+            if isinstance(node, ast.Import):
+                names = [a.name for a in node.names]
+            elif isinstance(node, ast.ImportFrom):
+                names = [node.module or ""]
+            assert not any(n.split(".")[0] == "oracle" for n in names), f"{path} imports the oracle"
+
+
+def test_missing_library_fails_loudly(monkeypatch: pytest.MonkeyPatch, tmp_path: Any) -> None:
+    from deciax_amd import _lib
+
+    monkeypatch.setattr(_lib, "_LIB", None)
+    monkeypatch.setattr(_lib, "LIB_PATH", tmp_path / "absent.so")
+    with pytest.raises(RuntimeError, match="missing"):
+        _lib.lib()
+    assert isinstance(ctypes.CDLL, type)
+
+
+# ----------------------------------------------------------------------------- impl seam
+
+
+def test_resolve_rejects_like_the_reference() -> None:
+    """Unknown impls raise ValueError (src/deciax/ops/backend.py:18); the reference's own backends are
+    not served here; without a gfx950 device `hip` is refused (src/deciax/models/clef/model.py:46-50)."""
+    import torch
+
+    from deciax_amd.backend import resolve
+
+    with pytest.raises(ValueError, match="must be"):
+        resolve("cuda")  # type: ignore[arg-type]
+    for impl in ("jax", "pallas"):
+        with pytest.raises(ValueError, match="reference"):
+            resolve(impl)  # type: ignore[arg-type]
+    if not torch.cuda.is_available():
+        with pytest.raises(ValueError, match="gfx950"):
+            resolve("hip")
+
+
+def test_load_validates_arguments() -> None:
+    import deciax_amd
+
+    with pytest.raises(ValueError, match="unknown model"):
+        deciax_amd.load("clef-27b")  # type: ignore[arg-type]
+    with pytest.raises(ValueError, match="revisions"):
+        deciax_amd.load("tiny", revision="main")
+    with pytest.raises(ValueError, match="bf16"):
+        deciax_amd.load("tiny", dtype="fp32")
+    with pytest.raises(ValueError):
+        deciax_amd.load("tiny", impl="nope")  # type: ignore[arg-type]
+
+
+# ----------------------------------------------------------------------------- schema
+
+
+@pytest.fixture
+def tokenizer() -> Any:
+    from tokenizers import Tokenizer, models, pre_tokenizers
+
+    from deciax_amd.schema import HFTokenizer
+
+    tok = Tokenizer(models.WordLevel({"[UNK]": 0, "hello": 1, "world": 2}, unk_token="[UNK]"))
+    tok.pre_tokenizer = pre_tokenizers.Whitespace()
+    return HFTokenizer(tok)
+
+
+QUESTIONS = {
+    "sentiment": {"type": "choice", "criteria": {"z": "world", "a": "hello"}},
+    "yes": {"type": "noul"},
+    "score": {"type": "score", "criteria": ["hello", "world", "hello world"]},
+}
+
+
+def test_encode_spans_and_option_order(tokenizer: Any) -> None:
+    """tests/clef/test_input.py:17-45: options sorted for choice, (true, false) for noul; spans
+    inside the record; the readout position is the last token of each option span."""
+    from deciax_amd.schema import encode, readout_layout
+
+    records = [encode(tokenizer, s, QUESTIONS, 512) for s in ("hello", "hello world " * 20)]
+    assert records[0].fields[0].option_ids == ("a", "z")
+    assert records[0].fields[1].option_ids == ("true", "false")
+    for record in records:
+        for field in record.fields:
+            assert field.span[0] < field.span[1] < len(record.ids)
+            for (start, end), (pos, _label) in zip(field.option_spans, field.readout()):
+                assert start < end <= len(record.ids) and pos == end - 1
+        assert sum(len(f.option_ids) for f in record.fields) == 7
+    layout = readout_layout(records)
+    assert [len(q) for q in layout[0]] == [2, 2, 3]
+
+
+def test_decode_kats(tokenizer: Any) -> None:
+    """Zero logits -> noul 0.5 and score 1.0 (tests/clef/test_input.py:42-44); NaN ->
+    FloatingPointError (:78-83); usage counts the input tokens (:44)."""
+    from deciax_amd.schema import decode, encode
+
+    record = encode(tokenizer, "hello", QUESTIONS, 512)
+    result = decode(record, np.zeros(7), QUESTIONS, "tiny")
+    assert result["answers"]["yes"]["noul"] == 0.5
+    assert result["answers"]["score"]["score"] == 1.0
+    assert result["answers"]["sentiment"]["choice"] in ("z", "a")
+    assert result["usage"]["input_tokens"] == len(record.ids)
+    logits = np.array([0.0, 3.0, 2.0, -2.0, 0.0, 0.0, 5.0], np.float32)
+    result = decode(record, logits, QUESTIONS, "tiny")
+    assert result["answers"]["sentiment"]["choice"] == "z"
+    assert result["answers"]["yes"]["noul"] == pytest.approx(1 / (1 + np.exp(-4.0)), abs=1e-4)
+    with pytest.raises(FloatingPointError, match="non-finite"):
+        decode(encode(tokenizer, "hello", {"yes": {"type": "noul"}}, 512), np.array([np.nan, 0.0]),
+               {"yes": {"type": "noul"}}, "tiny")
+
+
+def test_truncation_keeps_schema_complete(tokenizer: Any) -> None:
+    """tests/clef/test_input.py:48-60."""
+    from deciax_amd.schema import encode
+
+    q = {"x": {"type": "choice", "criteria": {"a": "hello", "b": "world"}}}
+    fixed = encode(tokenizer, "", q, 512)
+    limit = len(fixed.ids) + 5
+    actual = encode(tokenizer, "hello world " * 500, q, limit)
+    assert len(actual.ids) == limit
+    for a, b in zip(actual.fields, fixed.fields, strict=True):
+        assert a.span == (b.span[0] + 5, b.span[1] + 5)
+    with pytest.raises(ValueError, match="schema requires"):
+        encode(tokenizer, "", q, len(fixed.ids) - 1)
+
+
+@pytest.mark.parametrize("questions", [
+    {},
+    {"q": {"type": []}},
+    {"q": {"type": "score", "criteria": []}},
+    {"q": {"type": "noul", "criteria": {"yes": "yes"}}},
+    {"q": {"type": "choice", "criteria": {"a": "a"}, "option_order": ["a"]}},
+    {f"q{i}": {"type": "noul"} for i in range(65)},
+])
+def test_invalid_schema(questions: Any) -> None:
+    """tests/clef/test_input.py:63-75, plus the 64-question limit (src/deciax/protocol/systemone.py:17)."""
+    from deciax_amd.schema import validate_questions
+
+    with pytest.raises(ValueError):
+        validate_questions(questions)
+
+
+# ----------------------------------------------------------------------------- packing
+
+
+def test_pack_batch_layout() -> None:
+    from deciax_amd.gemma import pack_batch
+
+    r = rng(0)
+    lengths = [5, 64, 65, 1]
+    ids = [r.integers(0, 100, n).tolist() for n in lengths]
+    options = [[[(n - 1, 7), (0, 8)]] for n in lengths]
+    b = pack_batch(ids, options, device="cpu")
+    assert b.rows == sum(lengths) and b.max_len == 65
+    np.testing.assert_array_equal(b.seq_start.numpy(), [0, 5, 69, 134])
+    np.testing.assert_array_equal(b.vt_start.numpy(), [0, 64, 128, 256])
+    assert b.vt_ld == 64 + 64 + 128 + 64
+    np.testing.assert_array_equal(b.positions.numpy(), np.concatenate([np.arange(n) for n in lengths]))
+    np.testing.assert_array_equal(b.ids.numpy(), np.concatenate(ids))
+    np.testing.assert_array_equal(b.opt_pos.numpy(), [4, 0, 68, 5, 133, 69, 134, 134])
+    np.testing.assert_array_equal(b.q_offsets.numpy(), [0, 2, 4, 6, 8])
+    with pytest.raises(ValueError, match="outside request"):
+        pack_batch([[1, 2]], [[[(2, 0)]]], device="cpu")
+    with pytest.raises(ValueError, match="at least one token"):
+        pack_batch([[]], [[]], device="cpu")
+
+
+def test_config_flop_counts() -> None:
+    """Linear FLOPs per token of the 9B shape (about 16.6 GFLOP) and the attention pair of the
+    layer-pair workload (2.750e11 FLOP per layer at B8 S2048 16x256)."""
+    from dataclasses import replace
+
+    from deciax_amd.gemma import CONFIGS
+
+    c = CONFIGS["gemma2-9b"]
+    assert c.linear_flops_per_token() == pytest.approx(16.65e9, rel=1e-2)
+    one = replace(c, layers=1, window=0)
+    assert one.attention_flops([2048] * 8) == pytest.approx(2.750e11, rel=1e-3)
+    assert c.query_scale == 1 / 16 and CONFIGS["gemma2-27b"].query_scale == pytest.approx(1 / 12)
