@@ -164,6 +164,7 @@ int dx_linear(const void *x, const void *w, void *y, int64_t m, int64_t n, int64
   SUPPORTED(k % 64 == 0, "linear: k=%ld must be a multiple of 64", (long)k);
   REQUIRE(ldx >= k && ldw >= k && ldy >= n && ldx % 8 == 0 && ldw % 8 == 0 && ldy % 8 == 0,
           "linear: leading dimensions must cover the row and be multiples of 8");
+  SUPPORTED(ldx <= DX_MAX_LD && ldw <= DX_MAX_LD, "linear: leading dimensions above %d", DX_MAX_LD);
   REQUIRE(aligned16(x) && aligned16(w) && aligned16(y), "linear: pointers must be 16-byte aligned");
   REQUIRE(out_dtype == DX_BF16 || out_dtype == DX_F32, "linear: unknown out dtype %d", out_dtype);
   if (m == 0) return DX_OK;
@@ -182,6 +183,7 @@ int dx_gated_linear(const void *x, const void *gate_up, void *act, int64_t m, in
   SUPPORTED(f % 128 == 0, "gated_linear: f=%ld must be a multiple of 128", (long)f);
   SUPPORTED(k % 64 == 0, "gated_linear: k=%ld must be a multiple of 64", (long)k);
   REQUIRE(ldx >= k && ld_act >= f && ldx % 8 == 0 && ld_act % 8 == 0, "gated_linear: bad leading dimensions");
+  SUPPORTED(ldx <= DX_MAX_LD && k <= DX_MAX_LD, "gated_linear: leading dimensions above %d", DX_MAX_LD);
   REQUIRE(aligned16(x) && aligned16(gate_up) && aligned16(act), "gated_linear: pointers must be 16-byte aligned");
   REQUIRE(activation == DX_ACT_GELU_TANH || activation == DX_ACT_SILU, "gated_linear: unknown activation %d",
           activation);

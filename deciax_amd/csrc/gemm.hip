@@ -2,14 +2,25 @@
 //
 // A is activations [M, K] and B is a weight in PyTorch [out, in] layout, so
 // both operands are K-contiguous and every MFMA operand is one 16-byte LDS
-// read. Block tile BM x BN x 64 over 4 waves (2 x 2), each wave BM/2 x BN/2 in
-// 32x32x16 MFMA blocks with fp32 accumulators. Two LDS stages; the next K tile
-// is fetched into registers while the current one feeds the MFMAs.
+// read. Block tile BM x 256 x 64 over 4 waves (2 x 2), one wave per SIMD; each
+// wave owns a BM/2 x 128 quadrant in 32x32x16 MFMA blocks with fp32
+// accumulators (a single wave saturates the matrix core with this shape).
+//
+// Data path, per thread and K tile: 16-byte chunks arrive through buffer loads
+// (the resource is based at the tile origin, so rows past M read as zero and
+// 32-bit offsets cover every supported shape) into registers one K tile ahead,
+// are written to the idle half of a double-buffered LDS tile, and are read back
+// as MFMA fragments, themselves double-buffered in registers one k-step ahead.
+// Each k-step is a scheduling region of its own in which the 16 MFMAs carry,
+// interleaved at fixed slots, that k-step's share of the chunk loads (one per
+// four MFMAs), the LDS writes of the next tile and the next fragment reads: the
+// address unit never receives a burst large enough to stall instruction issue,
+// which is what bounds this kernel when loads are issued in clumps.
 //
 // LDS layout: row-major [rows][64] bf16, 16-byte chunk c of row r stored at
-// chunk position c ^ ((r >> 1) & 7). A 32-lane operand read touches 32 rows at
-// one logical chunk; with a 128-byte row pitch the XOR spreads 16 consecutive
-// rows over all 16 chunk slots of a 256-byte bank line.
+// chunk position c ^ ((r >> 1) & 7): a 32-lane fragment read touches 32 rows
+// at one logical chunk, and the XOR spreads 16 consecutive rows over all 16
+// chunk slots of a 256-byte bank line (conflict-free on gfx950's 64 banks).
 //
 // Epilogues: bf16 store (staged through LDS for 16-byte row stores), fp32
 // store, and the gated activation for a gate|up weight packed in 64-row
@@ -22,6 +33,7 @@
 namespace {
 
 constexpr int BK = 64;
+constexpr int BN = 256;
 constexpr int THREADS = 256;
 
 enum { EPI_BF16 = 0, EPI_F32 = 1, EPI_GATED = 2 };
@@ -46,57 +58,53 @@ DX_DEVICE void tile_coords(int pid, int nblocks, int num_m, int num_n, int &tm, 
 
 DX_DEVICE int swz(int row, int chunk) { return row * 64 + ((chunk ^ ((row >> 1) & 7)) << 3); }
 
-template <int BM, int BN, int EPI>
+DX_DEVICE __amdgpu_buffer_rsrc_t make_rsrc(const uint16_t *base, long bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc((void *)base, (short)0, (int)bytes, 0x00020000);
+}
+
+template <int BM, int EPI>
 __global__ void __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(1, 1)))
-gemm_nt_kernel(const uint16_t *__restrict__ A, const uint16_t *__restrict__ B, void *__restrict__ C,
-               int M, int N, int K, long lda, long ldb, long ldc, int act) {
-  constexpr int TM = BM / 64;  // 32x32 blocks per wave along m
-  constexpr int TN = BN / 64;  // along n
-  constexpr int ACH = BM * BK / 8 / THREADS;
-  constexpr int BCH = BN * BK / 8 / THREADS;
+gemm_nt_kernel(const uint16_t *__restrict__ A, const uint16_t *__restrict__ B, void *__restrict__ C, int M, int N,
+               int K, long lda, long ldb, long ldc, int act) {
+  constexpr int TM = BM / 64, TN = BN / 64;  // 32x32 blocks per wave along m, n
   constexpr int STAGE = (BM + BN) * BK;
+  constexpr int AC = BM * BK / 8 / THREADS, BC = BN * BK / 8 / THREADS;  // 16-byte chunks per thread
+  constexpr int NC = AC + BC;
+  constexpr int RATIO = NC / AC;  // chunk j is an A chunk iff j % RATIO == 0
+  static_assert(NC % 4 == 0 && NC % AC == 0, "chunk schedule");
   constexpr int OUT_W = EPI == EPI_GATED ? BN / 2 : BN;
   constexpr int OUT_PITCH = OUT_W + 8;
   constexpr int SMEM = (2 * STAGE > BM * OUT_PITCH) ? 2 * STAGE : BM * OUT_PITCH;
-  __shared__ __attribute__((aligned(16))) uint16_t smem[SMEM];
+  __shared__ __attribute__((aligned(1024))) uint16_t smem[SMEM];
 
   const int num_m = (M + BM - 1) / BM, num_n = N / BN;
   int tm, tn;
   tile_coords(blockIdx.x, gridDim.x, num_m, num_n, tm, tn);
   const int m0 = tm * BM, n0 = tn * BN;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 1, wn = wave & 1;
 
-  const uint16_t *a_src[ACH];
-  const uint16_t *b_src[BCH];
-  int a_dst[ACH], b_dst[BCH];
+  const __amdgpu_buffer_rsrc_t ra = make_rsrc(A + (long)m0 * lda, (long)min(M - m0, BM) * lda * 2);
+  const __amdgpu_buffer_rsrc_t rb = make_rsrc(B + (long)n0 * ldb, (long)BN * ldb * 2);
+  int voff[NC], dst[NC];
 #pragma unroll
-  for (int j = 0; j < ACH; ++j) {
-    const int id = tid + THREADS * j, row = id >> 3, c = id & 7;
-    const int grow = min(m0 + row, M - 1);  // tail rows re-read the last row; never stored
-    a_src[j] = A + (long)grow * lda + c * 8;
-    a_dst[j] = swz(row, c);
+  for (int j = 0; j < NC; ++j) {
+    const bool isa = j % RATIO == 0;
+    const int jj = isa ? j / RATIO : j - j / RATIO - 1;
+    const int id = tid + THREADS * jj, row = id >> 3, c = id & 7;
+    voff[j] = (int)((isa ? row * lda : row * ldb) * 2 + c * 16);
+    dst[j] = (isa ? 0 : BM * BK) + swz(row, c);
   }
+  u32x4 rg[NC];
+  auto gl = [&](int kt, int j0, int j1) {
 #pragma unroll
-  for (int j = 0; j < BCH; ++j) {
-    const int id = tid + THREADS * j, row = id >> 3, c = id & 7;
-    b_src[j] = B + (long)(n0 + row) * ldb + c * 8;
-    b_dst[j] = BM * BK + swz(row, c);
-  }
-
-  u32x4 ra[ACH], rb[BCH];
-  auto gload = [&](int kt) {
-#pragma unroll
-    for (int j = 0; j < ACH; ++j) ra[j] = *reinterpret_cast<const u32x4 *>(a_src[j] + kt * BK);
-#pragma unroll
-    for (int j = 0; j < BCH; ++j) rb[j] = *reinterpret_cast<const u32x4 *>(b_src[j] + kt * BK);
+    for (int j = j0; j < j1; ++j)
+      rg[j] = __builtin_bit_cast(u32x4,
+                                 __builtin_amdgcn_raw_buffer_load_b128(j % RATIO == 0 ? ra : rb, voff[j], kt * BK * 2, 0));
   };
-  auto sstore = [&](int stage) {
-    uint16_t *base = smem + stage * STAGE;
+  auto sw = [&](int stage, int j0, int j1) {
 #pragma unroll
-    for (int j = 0; j < ACH; ++j) *reinterpret_cast<u32x4 *>(base + a_dst[j]) = ra[j];
-#pragma unroll
-    for (int j = 0; j < BCH; ++j) *reinterpret_cast<u32x4 *>(base + b_dst[j]) = rb[j];
+    for (int j = j0; j < j1; ++j) *reinterpret_cast<u32x4 *>(smem + stage * STAGE + dst[j]) = rg[j];
   };
 
   floatx16 acc[TM][TN];
@@ -108,40 +116,86 @@ gemm_nt_kernel(const uint16_t *__restrict__ A, const uint16_t *__restrict__ B, v
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
   const int lrow = lane & 31, lhalf = lane >> 5;
-  auto compute = [&](int stage) {
+  bf16x8 fa0[TM], fb0[TN], fa1[TM], fb1[TN];
+  auto rd = [&](bf16x8 *fa, bf16x8 *fb, int stage, int ks) {
     const uint16_t *sa = smem + stage * STAGE;
     const uint16_t *sb = sa + BM * BK;
+    const int c = ks * 2 + lhalf;
 #pragma unroll
-    for (int ks = 0; ks < BK / 16; ++ks) {
-      const int c = ks * 2 + lhalf;
-      bf16x8 af[TM], bfr[TN];
+    for (int i = 0; i < TM; ++i)
+      fa[i] = as_bf16x8(*reinterpret_cast<const u32x4 *>(sa + swz(wm * (BM / 2) + i * 32 + lrow, c)));
 #pragma unroll
-      for (int i = 0; i < TM; ++i) {
-        const int row = wm * (BM / 2) + i * 32 + lrow;
-        af[i] = as_bf16x8(*reinterpret_cast<const u32x4 *>(sa + swz(row, c)));
-      }
+    for (int j = 0; j < TN; ++j)
+      fb[j] = as_bf16x8(*reinterpret_cast<const u32x4 *>(sb + swz(wn * (BN / 2) + j * 32 + lrow, c)));
+  };
+  auto mm = [&](const bf16x8 *fa, const bf16x8 *fb) {
 #pragma unroll
-      for (int j = 0; j < TN; ++j) {
-        const int row = wn * (BN / 2) + j * 32 + lrow;
-        bfr[j] = as_bf16x8(*reinterpret_cast<const u32x4 *>(sb + swz(row, c)));
-      }
+    for (int i = 0; i < TM; ++i)
 #pragma unroll
-      for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int j = 0; j < TN; ++j) acc[i][j] = mfma32(af[i], bfr[j], acc[i][j]);
-    }
+      for (int j = 0; j < TN; ++j) acc[i][j] = mfma32(fa[i], fb[j], acc[i][j]);
   };
 
+  // One k-step region: NM MFMAs; nw LDS writes in the first slots, one load after every GS
+  // MFMAs, the NR fragment reads from slot R0 on.
+  constexpr int NR = TM + TN, NM = TM * TN;
+  constexpr int NG = NC / 4;                           // chunk loads per k-step
+  constexpr int GS = NM / NG;                          // MFMAs between two loads
+  constexpr int W0 = (NC + 2) / 3, W1 = (NC + 1) / 3;  // writes per pre-barrier k-step
+  constexpr int R0 = NM / 4;                           // first fragment-read slot
+  static_assert(GS >= 2 && W0 <= NM && R0 + NR <= NM, "region schedule");
+#define DX_REGION(nw, ng)                                                                          \
+  do {                                                                                             \
+    _Pragma("unroll") for (int t = 0; t < NM; ++t) {                                               \
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                                           \
+      if (t < (nw)) __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);                             \
+      if (t % GS == GS - 1 && t / GS < (ng)) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);    \
+      if (t >= R0 && t - R0 < NR) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);               \
+    }                                                                                              \
+  } while (0)
+
   const int KT = K / BK;
-  gload(0);
-  sstore(0);
+  gl(0, 0, NC);
+  sw(0, 0, NC);
+  gl(min(1, KT - 1), 0, NC);
   __syncthreads();
+  rd(fa0, fb0, 0, 0);
   for (int kt = 0; kt < KT; ++kt) {
-    if (kt + 1 < KT) gload(kt + 1);
-    compute(kt & 1);
-    if (kt + 1 < KT) sstore((kt + 1) & 1);
-    __syncthreads();
+    // tile kt is in stage kt & 1; the registers hold tile kt + 1, which goes to the other stage
+    // while the registers refill with tile kt + 2 (clamped: the last tiles reload themselves).
+    const int st = kt & 1;
+    const int k2 = min(kt + 2, KT - 1);
+    __builtin_amdgcn_sched_barrier(0);
+    sw(st ^ 1, 0, W0);
+    gl(k2, 0, NG);
+    rd(fa1, fb1, st, 1);
+    mm(fa0, fb0);
+    DX_REGION(W0, NG);
+    __builtin_amdgcn_sched_barrier(0);
+    sw(st ^ 1, W0, W0 + W1);
+    gl(k2, NG, 2 * NG);
+    rd(fa0, fb0, st, 2);
+    mm(fa1, fb1);
+    DX_REGION(W1, NG);
+    __builtin_amdgcn_sched_barrier(0);
+    sw(st ^ 1, W0 + W1, NC);
+    gl(k2, 2 * NG, 3 * NG);
+    rd(fa1, fb1, st, 3);
+    mm(fa0, fb0);
+    DX_REGION(NC - W0 - W1, NG);
+    __builtin_amdgcn_sched_barrier(0);
+    // every wave's writes of tile kt + 1 and reads of tile kt are complete past this point
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    gl(k2, 3 * NG, NC);
+    rd(fa0, fb0, st ^ 1, 0);
+    mm(fa1, fb1);
+    DX_REGION(0, NG);
+    __builtin_amdgcn_sched_barrier(0);
   }
+#undef DX_REGION
+  asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+  __syncthreads();
 
   if constexpr (EPI == EPI_F32) {
     float *Cf = reinterpret_cast<float *>(C);
@@ -155,7 +209,6 @@ gemm_nt_kernel(const uint16_t *__restrict__ A, const uint16_t *__restrict__ B, v
           const int col = n0 + wn * (BN / 2) + j * 32 + lrow;
           if (row < M) Cf[(long)row * ldc + col] = acc[i][j][r];
         }
-    return;
   } else {
     // Stage the bf16 tile through LDS, then store 16-byte row chunks.
 #pragma unroll
@@ -194,11 +247,11 @@ gemm_nt_kernel(const uint16_t *__restrict__ A, const uint16_t *__restrict__ B, v
   }
 }
 
-template <int BM, int BN, int EPI>
+template <int BM, int EPI>
 hipError_t launch(const uint16_t *A, const uint16_t *B, void *C, long M, long N, long K, long lda, long ldb,
                   long ldc, int act, hipStream_t s) {
   const long num_m = (M + BM - 1) / BM, num_n = N / BN;
-  gemm_nt_kernel<BM, BN, EPI><<<dim3((unsigned)(num_m * num_n)), dim3(THREADS), 0, s>>>(
+  gemm_nt_kernel<BM, EPI><<<dim3((unsigned)(num_m * num_n)), dim3(THREADS), 0, s>>>(
       A, B, C, (int)M, (int)N, (int)K, lda, ldb, ldc, act);
   return hipGetLastError();
 }
@@ -207,8 +260,8 @@ template <int EPI>
 hipError_t dispatch(const uint16_t *A, const uint16_t *B, void *C, long M, long N, long K, long lda, long ldb,
                     long ldc, int act, hipStream_t s) {
   // Small M: halve the row tile so more workgroups exist.
-  if (M <= 1024) return launch<128, 256, EPI>(A, B, C, M, N, K, lda, ldb, ldc, act, s);
-  return launch<256, 256, EPI>(A, B, C, M, N, K, lda, ldb, ldc, act, s);
+  if (M <= 1024) return launch<128, EPI>(A, B, C, M, N, K, lda, ldb, ldc, act, s);
+  return launch<256, EPI>(A, B, C, M, N, K, lda, ldb, ldc, act, s);
 }
 
 }  // namespace

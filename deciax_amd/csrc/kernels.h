@@ -5,6 +5,10 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+// GEMM operands are addressed through buffer resources based at the tile origin with 32-bit byte
+// offsets: 256 rows of a leading dimension up to this many elements stay below 2^31 bytes.
+#define DX_MAX_LD (1 << 22)
+
 hipError_t dx_gemm_bf16(const uint16_t *A, const uint16_t *B, uint16_t *C, long M, long N, long K, long lda,
                         long ldb, long ldc, hipStream_t s);
 hipError_t dx_gemm_f32(const uint16_t *A, const uint16_t *B, float *C, long M, long N, long K, long lda, long ldb,
