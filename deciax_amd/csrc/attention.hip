@@ -34,8 +34,9 @@
 
 namespace {
 
-constexpr int THREADS = 256;
-constexpr int WAVES = 4;
+constexpr int THREADS = 256;        // fp32 path and the V^T transpose
+constexpr int BF_WAVES = 8;         // bf16 path: two waves per SIMD
+constexpr int BF_THREADS = 64 * BF_WAVES;
 constexpr int BKV = 64;
 constexpr float LOG2E = 1.4426950408889634f;
 constexpr float NEG_BIG = -1e30f;  // the reference's MASK_FILL (reference.py:8)
@@ -64,23 +65,48 @@ DX_DEVICE int vt_off(int row, int chunk) { return row * 64 + ((chunk ^ ((row >> 
 // lane-half hh then holds key 16 (r >> 3) + 8 hh + (r & 7).
 DX_DEVICE int kperm(int vk) { return 16 * (vk >> 4) + 8 * ((vk >> 2) & 1) + 4 * ((vk >> 3) & 1) + (vk & 3); }
 
+// Direct-to-LDS loads: instruction j of a wave's share fills 1 KB of LDS (64 lanes x 16 bytes) at a
+// wave-uniform base; each lane fetches the global chunk whose swizzled slot it fills.
+typedef __attribute__((address_space(3))) void lds_void;
+
+DX_DEVICE __amdgpu_buffer_rsrc_t make_rsrc(const uint16_t *base, long bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc((void *)base, (short)0, (int)bytes, 0x00020000);
+}
+
+// 16 bytes per lane from a buffer resource into LDS at lds + 16 * lane. The builtin is compiled in the
+// device pass only: this clang drops a kernel's host-side symbols when the host pass sees it.
+DX_DEVICE void lds_load16(__amdgpu_buffer_rsrc_t rsrc, uint16_t *lds, int voffset) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void *)lds, 16, voffset, 0, 0, 0);
+#endif
+}
+
+template <int D>
+DX_DEVICE int k_swz(int row) {
+  if constexpr (D / 8 >= 16) return row & 15;
+  else return (row >> 1) & 7;
+}
+
+// bf16 path: 8 waves (two per SIMD), wave w = 32 query rows of head g * G + w % G. Each 64-key tile is
+// processed in two 32-key halves (QK^T, softmax, PV per half) so a wave needs only 16 score registers and
+// the other wave on its SIMD can run MFMAs while this one is in the softmax.
 template <int D, int G, int MODE>
-__global__ void __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(1, 1)))
+__global__ void __launch_bounds__(BF_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2)))
 attn_bf16_kernel(const uint16_t *__restrict__ Q, const uint16_t *__restrict__ K, const uint16_t *__restrict__ Vt,
                  uint16_t *__restrict__ O, const int32_t *__restrict__ seq_start,
                  const int32_t *__restrict__ seq_len, const int32_t *__restrict__ vt_start, long vt_seq_stride,
                  int max_seq_len, long q_stride, long k_stride, long vt_ld, long o_stride, float scale,
                  float softcap, int window, int causal) {
-  constexpr int RG = WAVES / G;  // 32-row groups per head
+  constexpr int RG = BF_WAVES / G;  // 32-row groups per head
   constexpr int BQ = 32 * RG;    // query rows per workgroup
-  constexpr int KST = BKV * D;
+  constexpr int KST = BKV * D;   // elements of the K tile
   constexpr int STAGE = 2 * BKV * D;
-  constexpr int KCH = BKV * D / 8 / THREADS;
-  constexpr int VCH = D * BKV / 8 / THREADS;
+  constexpr int KI = BKV * D / 8 / 64 / BF_WAVES;  // direct-to-LDS instructions per wave for K (and for V^T)
   constexpr int NKS = D / 16;
   constexpr int NDB = D / 32;
   constexpr int CPR = D / 8;  // 16-byte chunks per K row
-  __shared__ __attribute__((aligned(16))) uint16_t smem[2 * STAGE];
+  static_assert(KI >= 1, "tile too small for the wave count");
+  __shared__ __attribute__((aligned(1024))) uint16_t smem[2 * STAGE];
 
   const int b = blockIdx.y, g = blockIdx.z;
   const int len = min(max(seq_len[b], 0), max_seq_len);
@@ -90,9 +116,9 @@ attn_bf16_kernel(const uint16_t *__restrict__ Q, const uint16_t *__restrict__ K,
   const long start = seq_start[b];
   const long vts = vt_start ? (long)vt_start[b] : (long)b * vt_seq_stride;
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lrow = lane & 31, lhalf = lane >> 5;
-  const int rg = wave % RG, h = g * G + wave / RG;
+  const int rg = wave / G, h = g * G + wave % G;
   const int qw0 = q0 + rg * 32, qw1 = qw0 + 31;
   const int qi = qw0 + lrow;
 
@@ -114,34 +140,27 @@ attn_bf16_kernel(const uint16_t *__restrict__ Q, const uint16_t *__restrict__ K,
   }
   const int kt0 = klo / BKV, kt1 = (khi + BKV - 1) / BKV;
 
-  const uint16_t *kbase = K + start * k_stride + (long)g * D;
-  const uint16_t *vbase = Vt + (long)g * D * vt_ld + vts;
-  u32x4 rk[KCH], rv[VCH];
-  auto gload = [&](int kt) {
+  // K rows past len read as zero (outside the resource); V^T columns stay inside this sequence's
+  // 64-aligned block, whose tail dx_transpose_v zero-fills.
+  const __amdgpu_buffer_rsrc_t rk = make_rsrc(K + start * k_stride + (long)g * D, (long)len * k_stride * 2);
+  const __amdgpu_buffer_rsrc_t rv = make_rsrc(Vt + (long)g * D * vt_ld + vts, ((long)(D - 1) * vt_ld + ((len + 63) & ~63)) * 2);
+  int kvo[KI], vvo[KI];
 #pragma unroll
-    for (int j = 0; j < KCH; ++j) {
-      const int id = tid + THREADS * j, row = id / CPR, c = id % CPR;
-      const int key = min(kt * BKV + row, len - 1);
-      rk[j] = *reinterpret_cast<const u32x4 *>(kbase + (long)key * k_stride + c * 8);
-    }
-#pragma unroll
-    for (int j = 0; j < VCH; ++j) {
-      const int id = tid + THREADS * j, row = id >> 3, c = id & 7;
-      rv[j] = *reinterpret_cast<const u32x4 *>(vbase + (long)row * vt_ld + kt * BKV + c * 8);
-    }
-  };
-  auto sstore = [&](int st) {
+  for (int j = 0; j < KI; ++j) {
+    const int p = (wave * KI + j) * 64 + lane;  // physical 16-byte slot in the tile
+    const int krow = p / CPR, kc = (p % CPR) ^ k_swz<D>(krow);
+    kvo[j] = (int)(((long)krow * k_stride + kc * 8) * 2);
+    const int vrow = p >> 3, vc = (p & 7) ^ ((vrow >> 1) & 7);
+    vvo[j] = (int)(((long)vrow * vt_ld + vc * 8) * 2);
+  }
+  auto issue = [&](int kt, int st) {
     uint16_t *base = smem + st * STAGE;
+    // tile offsets go into the range-checked VGPR offset, so K rows past len read as zero
 #pragma unroll
-    for (int j = 0; j < KCH; ++j) {
-      const int id = tid + THREADS * j, row = id / CPR, c = id % CPR;
-      *reinterpret_cast<u32x4 *>(base + k_off<D>(row, c)) = rk[j];
-    }
+    for (int j = 0; j < KI; ++j)
+      lds_load16(rk, base + (wave * KI + j) * 512, kvo[j] + (int)((long)kt * BKV * k_stride * 2));
 #pragma unroll
-    for (int j = 0; j < VCH; ++j) {
-      const int id = tid + THREADS * j, row = id >> 3, c = id & 7;
-      *reinterpret_cast<u32x4 *>(base + KST + vt_off(row, c)) = rv[j];
-    }
+    for (int j = 0; j < KI; ++j) lds_load16(rv, base + KST + (wave * KI + j) * 512, vvo[j] + kt * BKV * 2);
   };
 
   floatx16 o[NDB];
@@ -156,74 +175,68 @@ attn_bf16_kernel(const uint16_t *__restrict__ Q, const uint16_t *__restrict__ K,
   const float c2 = -2.f * LOG2E * softcap;
   const float c3 = 0.5f * LOG2E * softcap;
 
-  gload(kt0);
-  sstore(0);
+  issue(kt0, 0);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
   for (int kt = kt0; kt < kt1; ++kt) {
     const int st = (kt - kt0) & 1;
-    if (kt + 1 < kt1) gload(kt + 1);
+    if (kt + 1 < kt1) issue(kt + 1, st ^ 1);
     const int key0 = kt * BKV;
+    const uint16_t *sk = smem + st * STAGE;
+    const uint16_t *sv = sk + KST;
 
-    bool active = qw0 < len;
-    bool need_mask = key0 + BKV > len;
-    if (causal) {
-      active = active && key0 <= qw1 && !(window > 0 && key0 + BKV - 1 <= qw0 - window);
-      need_mask = need_mask || key0 + BKV - 1 > qw0 || (window > 0 && key0 <= qw1 - window);
-    } else if (window > 0) {
-      active = active && key0 <= qw1 + window && key0 + BKV - 1 >= qw0 - window;
-      need_mask = need_mask || key0 < qw1 - window || key0 + BKV - 1 > qw0 + window;
-    }
-
-    if (active) {
-      const uint16_t *sk = smem + st * STAGE;
-      const uint16_t *sv = sk + KST;
-      floatx16 s[2];
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) s[kb][r] = 0.f;
-        const int krow = kb * 32 + kperm(lrow);
-#pragma unroll
-        for (int ks = 0; ks < NKS; ++ks)
-          s[kb] = mfma32(as_bf16x8(*reinterpret_cast<const u32x4 *>(sk + k_off<D>(krow, ks * 2 + lhalf))), qf[ks],
-                         s[kb]);
+    for (int kb = 0; kb < 2; ++kb) {
+      const int kbase = key0 + kb * 32;
+      bool active = qw0 < len;
+      bool need_mask = kbase + 32 > len;
+      if (causal) {
+        active = active && kbase <= qw1 && !(window > 0 && kbase + 31 <= qw0 - window);
+        need_mask = need_mask || kbase + 31 > qw0 || (window > 0 && kbase <= qw1 - window);
+      } else if (window > 0) {
+        active = active && kbase <= qw1 + window && kbase + 31 >= qw0 - window;
+        need_mask = need_mask || kbase < qw1 - window || kbase + 31 > qw0 + window;
       }
+      if (!active) continue;
 
-      uint32_t vis = 0xffffffffu;  // bit kb * 16 + r
+      floatx16 s;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) s[r] = 0.f;
+      const int krow = kb * 32 + kperm(lrow);
+#pragma unroll
+      for (int ks = 0; ks < NKS; ++ks)
+        s = mfma32(as_bf16x8(*reinterpret_cast<const u32x4 *>(sk + krow * D + (((ks * 2 + lhalf) ^ k_swz<D>(krow)) << 3))),
+                   qf[ks], s);
+
+      uint32_t vis = 0xffffu;  // bit r: key kbase + 16 (r >> 3) + 8 lhalf + (r & 7)
       if (need_mask) {
         vis = 0;
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int key = key0 + kb * 32 + 16 * (r >> 3) + 8 * lhalf + (r & 7);
-            vis |= (uint32_t)visible(qi, key, len, window, causal) << (kb * 16 + r);
-          }
+        for (int r = 0; r < 16; ++r) {
+          const int key = kbase + 16 * (r >> 3) + 8 * lhalf + (r & 7);
+          vis |= (uint32_t)visible(qi, key, len, window, causal) << r;
+        }
       }
 
       if constexpr (MODE == MODE_FIXED) {
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const float e = fast_exp2(s[kb][r] * c1);
-            const float p = fast_exp2(c3 + c2 * fast_rcp(1.f + e));
-            s[kb][r] = ((vis >> (kb * 16 + r)) & 1u) ? p : 0.f;
-            lsum += s[kb][r];
-          }
+        for (int r = 0; r < 16; ++r) {
+          const float e = fast_exp2(s[r] * c1);
+          const float p = fast_exp2(c3 + c2 * fast_rcp(1.f + e));
+          s[r] = ((vis >> r) & 1u) ? p : 0.f;
+          lsum += s[r];
+        }
       } else {
         float tmax = NEG_BIG;
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            float t = s[kb][r] * scale;
-            if (softcap > 0.f) t = softcap * tanhf(t / softcap);
-            t *= LOG2E;
-            t = ((vis >> (kb * 16 + r)) & 1u) ? t : NEG_BIG;
-            s[kb][r] = t;
-            tmax = fmaxf(tmax, t);
-          }
+        for (int r = 0; r < 16; ++r) {
+          float t = s[r] * scale;
+          if (softcap > 0.f) t = softcap * tanhf(t / softcap);
+          t *= LOG2E;
+          t = ((vis >> r) & 1u) ? t : NEG_BIG;
+          s[r] = t;
+          tmax = fmaxf(tmax, t);
+        }
         tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
         const float mnew = fmaxf(mrun, tmax);
         const float alpha = fast_exp2(mrun - mnew);
@@ -234,50 +247,46 @@ attn_bf16_kernel(const uint16_t *__restrict__ Q, const uint16_t *__restrict__ K,
 #pragma unroll
           for (int r = 0; r < 16; ++r) o[i][r] *= alpha;
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const float p = ((vis >> (kb * 16 + r)) & 1u) ? fast_exp2(s[kb][r] - mnew) : 0.f;
-            s[kb][r] = p;
-            lsum += p;
-          }
+        for (int r = 0; r < 16; ++r) {
+          const float p = ((vis >> r) & 1u) ? fast_exp2(s[r] - mnew) : 0.f;
+          s[r] = p;
+          lsum += p;
+        }
       }
 
-      bf16x8 pf[4];
+      bf16x8 pf[2];
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
+      for (int h2 = 0; h2 < 2; ++h2) {
+        u32x4 w;
 #pragma unroll
-        for (int h2 = 0; h2 < 2; ++h2) {
-          u32x4 w;
-#pragma unroll
-          for (int i = 0; i < 4; ++i) w[i] = pack_bf2(s[kb][8 * h2 + 2 * i], s[kb][8 * h2 + 2 * i + 1]);
-          pf[kb * 2 + h2] = as_bf16x8(w);
-        }
+        for (int i = 0; i < 4; ++i) w[i] = pack_bf2(s[8 * h2 + 2 * i], s[8 * h2 + 2 * i + 1]);
+        pf[h2] = as_bf16x8(w);
+      }
 #pragma unroll
       for (int db = 0; db < NDB; ++db) {
         const int vrow = db * 32 + lrow;
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-          for (int h2 = 0; h2 < 2; ++h2)
-            o[db] = mfma32(as_bf16x8(*reinterpret_cast<const u32x4 *>(sv + vt_off(vrow, kb * 4 + 2 * h2 + lhalf))),
-                           pf[kb * 2 + h2], o[db]);
+        for (int h2 = 0; h2 < 2; ++h2)
+          o[db] = mfma32(as_bf16x8(*reinterpret_cast<const u32x4 *>(sv + vt_off(vrow, kb * 4 + 2 * h2 + lhalf))),
+                         pf[h2], o[db]);
       }
     }
-    if (kt + 1 < kt1) sstore(st ^ 1);
+    // the next tile has landed in every wave's share and every wave is done reading this one
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
   }
 
   lsum += __shfl_xor(lsum, 32, 64);
   if (qi < len) {
+    const float inv = 1.f / lsum;
     uint16_t *op = O + (start + qi) * o_stride + (long)h * D + lhalf * 4;
 #pragma unroll
     for (int db = 0; db < NDB; ++db)
 #pragma unroll
       for (int grp = 0; grp < 4; ++grp) {
         u32x2 w;
-        w[0] = pack_bf2(o[db][grp * 4 + 0] / lsum, o[db][grp * 4 + 1] / lsum);
-        w[1] = pack_bf2(o[db][grp * 4 + 2] / lsum, o[db][grp * 4 + 3] / lsum);
+        w[0] = pack_bf2(o[db][grp * 4 + 0] * inv, o[db][grp * 4 + 1] * inv);
+        w[1] = pack_bf2(o[db][grp * 4 + 2] * inv, o[db][grp * 4 + 3] * inv);
         *reinterpret_cast<u32x2 *>(op + db * 32 + grp * 8) = w;
       }
   }
@@ -421,11 +430,11 @@ transpose_v_kernel(const uint16_t *__restrict__ V, uint16_t *__restrict__ Vt, co
 
 template <int D, int G>
 hipError_t launch_bf16_dg(const AttnArgs &a, hipStream_t s) {
-  constexpr int BQ = 32 * (WAVES / G);
+  constexpr int BQ = 32 * (BF_WAVES / G);
   const dim3 grid((a.max_seq_len + BQ - 1) / BQ, a.num_seqs, a.hkv);
   const bool fixed = a.softcap > 0.f && a.softcap <= 56.f;
   auto kern = fixed ? attn_bf16_kernel<D, G, MODE_FIXED> : attn_bf16_kernel<D, G, MODE_ONLINE>;
-  kern<<<grid, dim3(THREADS), 0, s>>>(
+  kern<<<grid, dim3(BF_THREADS), 0, s>>>(
       static_cast<const uint16_t *>(a.q), static_cast<const uint16_t *>(a.k), static_cast<const uint16_t *>(a.v),
       static_cast<uint16_t *>(a.out), a.seq_start, a.seq_len, a.vt_start, a.vt_seq_stride, a.max_seq_len,
       a.q_stride, a.k_stride, a.v_stride, a.out_stride, a.scale, a.softcap, a.window, a.causal);
