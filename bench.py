@@ -129,10 +129,26 @@ def algorithmic_work(cfg, lengths: list[int]) -> dict[str, float]:
     }
 
 
-def cpu_baseline(cfg, seconds_budget: float = 20.0) -> dict:
+TRAFFIC_PROFILES = {"gate_up_proj": ROOT / "profiles" / "gate_up_gemm_traffic.md"}
+
+
+def measured_traffic(kernel: str) -> float | None:
+    """HBM bytes per launch of `kernel` from its committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary
+    (counters scaled by a plain-copy calibration), or None when no such summary exists."""
+    path = TRAFFIC_PROFILES.get(kernel)
+    if path is None or not path.exists():
+        return None
+    for line in path.read_text().splitlines():
+        if line.startswith("traffic_bytes_per_launch:"):
+            return float(line.split(":", 1)[1])
+    return None
+
+
+def cpu_baseline(cfg, seconds_budget: float = 25.0, n: int = 2048) -> dict:
     """The oracle (numpy fp32 restatement of the path, bf16 rounding points) on a bounded sample:
-    one request of 512 tokens through one sliding and one global layer of the 9B shape plus the
-    readout; the measured FLOP rate is extrapolated to the full batch by its FLOP count."""
+    one request of n tokens through one sliding and one global layer of the 9B shape plus the
+    readout, up to 5 runs within the time budget; the measured FLOP rate is extrapolated to the
+    full batch by its FLOP count."""
     from oracle import model as om
 
     try:
@@ -141,7 +157,7 @@ def cpu_baseline(cfg, seconds_budget: float = 20.0) -> dict:
     except Exception:  # pragma: no cover
         threads = len(os.sched_getaffinity(0))
     r = np.random.Generator(np.random.PCG64(1))
-    n, layers = 512, 2
+    layers = 2
     shape = om.Shape(hidden=cfg.hidden, heads=cfg.heads, kv_heads=cfg.kv_heads, head_dim=cfg.head_dim,
                      intermediate=cfg.intermediate, vocab=cfg.vocab, layers=layers, window=cfg.window,
                      query_scale=cfg.query_scale)
@@ -247,7 +263,7 @@ def main() -> None:
         "peak": PEAK_BF16 / 1e12,
         "unit": "TFLOP/s",
         "frac": round(dom.get("frac_bf16_peak", 0.0), 4),
-        "traffic": None,
+        "traffic": measured_traffic(dominant),
         "algorithmic_flop_per_launch": work.get(dominant, 0.0),
     }
     attn_ms = sum(kern[k]["total_ms"] for k in kern if k.startswith("attention")) / args.steps

@@ -225,6 +225,50 @@ def random_weights(config: GemmaConfig, *, seed: int = 0, device: str | torch.de
     return DecisionWeights(c, embed, final_norm, layers, _bits_to_tensor(cos, dev), _bits_to_tensor(sin, dev))
 
 
+def weights_from_host(config: GemmaConfig, tensors: dict[str, np.ndarray | torch.Tensor], *,
+                      device: str | torch.device = "cuda", keep_unpacked: bool = False) -> DecisionWeights:
+    """Device weights from host arrays named as the oracle names them: `embed` [V, H], `final_norm`,
+    and per layer `layers.{i}.` + input_norm, q [Hq D, H], k, v [Hkv D, H], o [H, Hq D],
+    post_attn_norm, pre_ffn_norm, gate, up [I, H], down [H, I], post_ffn_norm (PyTorch [out, in]
+    layout, values rounded to bf16). q|k|v and gate|up are packed once here, as the reference packs
+    at load (src/deciax/models/clef/model.py:72-76, src/deciax/models/qwen3_5/pallas.py:28-59)."""
+    c = config
+    dev = torch.device(device)
+
+    def dev_bf16(name: str, shape: tuple[int, ...]) -> torch.Tensor:
+        if name not in tensors:
+            raise ValueError(f"missing weight {name!r}")
+        t = torch.as_tensor(np.asarray(tensors[name], np.float32) if not isinstance(tensors[name], torch.Tensor)
+                            else tensors[name])
+        if tuple(t.shape) != shape:
+            raise ValueError(f"weight {name!r} has shape {tuple(t.shape)}, expected {shape}")
+        return t.to(device=dev, dtype=BF16).contiguous()
+
+    h, d = c.hidden, c.head_dim
+    layers = []
+    for i in range(c.layers):
+        p = f"layers.{i}."
+        gate = dev_bf16(p + "gate", (c.intermediate, h))
+        up = dev_bf16(p + "up", (c.intermediate, h))
+        lw = LayerWeights(
+            input_norm=dev_bf16(p + "input_norm", (h,)),
+            qkv=torch.cat([dev_bf16(p + "q", (c.heads * d, h)), dev_bf16(p + "k", (c.kv_heads * d, h)),
+                           dev_bf16(p + "v", (c.kv_heads * d, h))]).contiguous(),
+            o=dev_bf16(p + "o", (h, c.heads * d)),
+            post_attn_norm=dev_bf16(p + "post_attn_norm", (h,)),
+            pre_ffn_norm=dev_bf16(p + "pre_ffn_norm", (h,)),
+            gate_up=K.pack_gate_up(gate, up),
+            down=dev_bf16(p + "down", (h, c.intermediate)),
+            post_ffn_norm=dev_bf16(p + "post_ffn_norm", (h,)),
+        )
+        if keep_unpacked:
+            lw.gate, lw.up = gate, up
+        layers.append(lw)
+    cos, sin = rope_tables(c.max_position, d, c.rope_theta)
+    return DecisionWeights(c, dev_bf16("embed", (c.vocab, h)), dev_bf16("final_norm", (h,)), layers,
+                           _bits_to_tensor(cos, dev), _bits_to_tensor(sin, dev))
+
+
 @dataclass
 class PackedBatch:
     """A varlen batch on the device.
