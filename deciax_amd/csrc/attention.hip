@@ -37,7 +37,8 @@ namespace {
 constexpr int THREADS = 256;        // fp32 path and the V^T transpose
 constexpr int BF_WAVES = 8;         // bf16 path: two waves per SIMD
 constexpr int BF_THREADS = 64 * BF_WAVES;
-constexpr int BKV = 64;
+constexpr int BKV = 64;     // V^T block alignment of dx_transpose_v
+constexpr int NSTAGE = 4;   // LDS ring depth of the bf16 path
 constexpr float LOG2E = 1.4426950408889634f;
 constexpr float NEG_BIG = -1e30f;  // the reference's MASK_FILL (reference.py:8)
 
@@ -49,17 +50,18 @@ DX_DEVICE bool visible(int qi, int key, int len, int window, int causal) {
   return window <= 0 || abs(qi - key) <= window;
 }
 
-// K tile in LDS: [64 keys][D], 16-byte chunk c of row r at a swizzled slot.
-template <int D>
-DX_DEVICE int k_off(int row, int chunk) {
-  if constexpr (D / 8 >= 16)
-    return row * D + ((chunk ^ (row & 15)) << 3);
-  else
-    return row * D + ((chunk ^ ((row >> 1) & 7)) << 3);
-}
+// K tile in LDS: [TK keys][D], 16-byte chunk c of row r at slot c ^ k_swz<D>(r) (see below).
 
-// V^T tile in LDS: [D][64 keys], 128-byte rows.
-DX_DEVICE int vt_off(int row, int chunk) { return row * 64 + ((chunk ^ ((row >> 1) & 7)) << 3); }
+// V^T tile in LDS: [D][T keys]; with 64-byte rows (T = 32) chunk c of row r sits at slot c ^ ((r >> 2) & 3),
+// with 128-byte rows (T = 64) at c ^ ((r >> 1) & 7): the 16 rows one fragment read touches per pass fill
+// all 16 chunk slots of a 256-byte bank line.
+template <int T>
+DX_DEVICE int vt_swz(int row) {
+  if constexpr (T == 32) return (row >> 2) & 3;
+  else return (row >> 1) & 7;  // 128-byte rows
+}
+template <int T>
+DX_DEVICE int vt_off(int row, int chunk) { return row * T + ((chunk ^ vt_swz<T>(row)) << 3); }
 
 // MFMA row vk of a 32-key block reads key kperm(vk). The output register r of
 // lane-half hh then holds key 16 (r >> 3) + 8 hh + (r & 7).
@@ -81,6 +83,20 @@ DX_DEVICE void lds_load16(__amdgpu_buffer_rsrc_t rsrc, uint16_t *lds, int voffse
 #endif
 }
 
+// Schedule n (LDS read, MFMA) pairs with the reads LEAD ahead: enough to cover LDS latency, few
+// enough that the operand registers in flight stay small.
+template <int N>
+DX_DEVICE void stream_sched() {
+  constexpr int LEAD = 3;
+  __builtin_amdgcn_sched_group_barrier(0x100, LEAD, 0);
+#pragma unroll
+  for (int t = 0; t < N - LEAD; ++t) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+  }
+  __builtin_amdgcn_sched_group_barrier(0x008, LEAD, 0);
+}
+
 template <int D>
 DX_DEVICE int k_swz(int row) {
   if constexpr (D / 8 >= 16) return row & 15;
@@ -90,6 +106,10 @@ DX_DEVICE int k_swz(int row) {
 // bf16 path: 8 waves (two per SIMD), wave w = 32 query rows of head g * G + w % G. Each 64-key tile is
 // processed in two 32-key halves (QK^T, softmax, PV per half) so a wave needs only 16 score registers and
 // the other wave on its SIMD can run MFMAs while this one is in the softmax.
+// Keys per tile: 32 at head_dim 256 (a 64-key tile would halve the ring depth), 64 below.
+template <int D>
+constexpr int tile_keys() { return D >= 256 ? 32 : 64; }
+
 template <int D, int G, int MODE>
 __global__ void __launch_bounds__(BF_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2)))
 attn_bf16_kernel(const uint16_t *__restrict__ Q, const uint16_t *__restrict__ K, const uint16_t *__restrict__ Vt,
@@ -97,16 +117,18 @@ attn_bf16_kernel(const uint16_t *__restrict__ Q, const uint16_t *__restrict__ K,
                  const int32_t *__restrict__ seq_len, const int32_t *__restrict__ vt_start, long vt_seq_stride,
                  int max_seq_len, long q_stride, long k_stride, long vt_ld, long o_stride, float scale,
                  float softcap, int window, int causal) {
-  constexpr int RG = BF_WAVES / G;  // 32-row groups per head
-  constexpr int BQ = 32 * RG;    // query rows per workgroup
-  constexpr int KST = BKV * D;   // elements of the K tile
-  constexpr int STAGE = 2 * BKV * D;
-  constexpr int KI = BKV * D / 8 / 64 / BF_WAVES;  // direct-to-LDS instructions per wave for K (and for V^T)
+  constexpr int TK = tile_keys<D>();
+  constexpr int RG = BF_WAVES / G;      // 32-row groups per head
+  constexpr int BQ = 32 * RG;           // query rows per workgroup
+  constexpr int KST = TK * D;           // elements of the K tile [TK][D]; the V^T tile [D][TK] follows
+  constexpr int STAGE = 2 * TK * D;
+  constexpr int NI = TK * D / 256;      // direct-to-LDS instructions per tile (K then V^T), 1 KB each
+  constexpr int WI = NI / BF_WAVES;     // per wave
   constexpr int NKS = D / 16;
   constexpr int NDB = D / 32;
-  constexpr int CPR = D / 8;  // 16-byte chunks per K row
-  static_assert(KI >= 1, "tile too small for the wave count");
-  __shared__ __attribute__((aligned(1024))) uint16_t smem[2 * STAGE];
+  constexpr int CPR = D / 8;            // 16-byte chunks per K row
+  static_assert(WI >= 1 && NI % BF_WAVES == 0, "tile too small for the wave count");
+  __shared__ __attribute__((aligned(1024))) uint16_t smem[NSTAGE * STAGE];
 
   const int b = blockIdx.y, g = blockIdx.z;
   const int len = min(max(seq_len[b], 0), max_seq_len);
@@ -138,29 +160,32 @@ attn_bf16_kernel(const uint16_t *__restrict__ Q, const uint16_t *__restrict__ K,
     khi = window > 0 ? min(len, qlast + window + 1) : len;
     klo = window > 0 ? max(0, q0 - window) : 0;
   }
-  const int kt0 = klo / BKV, kt1 = (khi + BKV - 1) / BKV;
+  const int kt0 = klo / TK, kt1 = (khi + TK - 1) / TK;
 
   // K rows past len read as zero (outside the resource); V^T columns stay inside this sequence's
   // 64-aligned block, whose tail dx_transpose_v zero-fills.
   const __amdgpu_buffer_rsrc_t rk = make_rsrc(K + start * k_stride + (long)g * D, (long)len * k_stride * 2);
   const __amdgpu_buffer_rsrc_t rv = make_rsrc(Vt + (long)g * D * vt_ld + vts, ((long)(D - 1) * vt_ld + ((len + 63) & ~63)) * 2);
-  int kvo[KI], vvo[KI];
-#pragma unroll
-  for (int j = 0; j < KI; ++j) {
-    const int p = (wave * KI + j) * 64 + lane;  // physical 16-byte slot in the tile
-    const int krow = p / CPR, kc = (p % CPR) ^ k_swz<D>(krow);
-    kvo[j] = (int)(((long)krow * k_stride + kc * 8) * 2);
-    const int vrow = p >> 3, vc = (p & 7) ^ ((vrow >> 1) & 7);
-    vvo[j] = (int)(((long)vrow * vt_ld + vc * 8) * 2);
-  }
+  // Instruction i < NI / 2 fills K slots [64 i, 64 i + 64): K row p / CPR, chunk (p % CPR) ^ k_swz(row).
+  // The others fill V^T slots: row p / (TK / 8), chunk (p % (TK / 8)) ^ vt_swz(row). Offsets are
+  // recomputed per issue (a few VALU ops) rather than held in registers.
+  const long ks2 = k_stride * 2, vl2 = vt_ld * 2;
   auto issue = [&](int kt, int st) {
     uint16_t *base = smem + st * STAGE;
-    // tile offsets go into the range-checked VGPR offset, so K rows past len read as zero
 #pragma unroll
-    for (int j = 0; j < KI; ++j)
-      lds_load16(rk, base + (wave * KI + j) * 512, kvo[j] + (int)((long)kt * BKV * k_stride * 2));
-#pragma unroll
-    for (int j = 0; j < KI; ++j) lds_load16(rv, base + KST + (wave * KI + j) * 512, vvo[j] + kt * BKV * 2);
+    for (int j = 0; j < WI; ++j) {
+      const int i = wave * WI + j;  // wave-uniform
+      if (i < NI / 2) {
+        const int p = i * 64 + lane;
+        const int krow = p / CPR, kc = (p % CPR) ^ k_swz<D>(krow);
+        // the tile offset goes into the range-checked VGPR offset, so K rows past len read as zero
+        lds_load16(rk, base + i * 512, (int)((kt * TK + krow) * ks2) + kc * 16);
+      } else {
+        const int p = (i - NI / 2) * 64 + lane;
+        const int vrow = p / (TK / 8), vc = (p % (TK / 8)) ^ vt_swz<TK>(vrow);
+        lds_load16(rv, base + KST + (i - NI / 2) * 512, (int)(vrow * vl2) + vc * 16 + kt * TK * 2);
+      }
+    }
   };
 
   floatx16 o[NDB];
@@ -175,30 +200,30 @@ attn_bf16_kernel(const uint16_t *__restrict__ Q, const uint16_t *__restrict__ K,
   const float c2 = -2.f * LOG2E * softcap;
   const float c3 = 0.5f * LOG2E * softcap;
 
-  issue(kt0, 0);
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  // Ring of NSTAGE tiles: tile kt sits in stage (kt - kt0) % NSTAGE, and tile kt + NSTAGE - 1 is
+  // fetched while tile kt is multiplied (clamped: the last tiles reload themselves harmlessly).
+#pragma unroll
+  for (int i = 0; i < NSTAGE - 1; ++i) issue(min(kt0 + i, kt1 - 1), i);
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"((NSTAGE - 2) * WI) : "memory");
   __syncthreads();
   for (int kt = kt0; kt < kt1; ++kt) {
-    const int st = (kt - kt0) & 1;
-    if (kt + 1 < kt1) issue(kt + 1, st ^ 1);
-    const int key0 = kt * BKV;
+    const int st = (kt - kt0) % NSTAGE;
+    issue(min(kt + NSTAGE - 1, kt1 - 1), (kt - kt0 + NSTAGE - 1) % NSTAGE);
     const uint16_t *sk = smem + st * STAGE;
     const uint16_t *sv = sk + KST;
+    auto half = [&](const int kb) {
+    const int kbase = kt * TK + kb * 32;
 
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-      const int kbase = key0 + kb * 32;
-      bool active = qw0 < len;
-      bool need_mask = kbase + 32 > len;
-      if (causal) {
-        active = active && kbase <= qw1 && !(window > 0 && kbase + 31 <= qw0 - window);
-        need_mask = need_mask || kbase + 31 > qw0 || (window > 0 && kbase <= qw1 - window);
-      } else if (window > 0) {
-        active = active && kbase <= qw1 + window && kbase + 31 >= qw0 - window;
-        need_mask = need_mask || kbase < qw1 - window || kbase + 31 > qw0 + window;
-      }
-      if (!active) continue;
-
+    bool active = qw0 < len;
+    bool need_mask = kbase + 32 > len;
+    if (causal) {
+      active = active && kbase <= qw1 && !(window > 0 && kbase + 31 <= qw0 - window);
+      need_mask = need_mask || kbase + 31 > qw0 || (window > 0 && kbase <= qw1 - window);
+    } else if (window > 0) {
+      active = active && kbase <= qw1 + window && kbase + 31 >= qw0 - window;
+      need_mask = need_mask || kbase < qw1 - window || kbase + 31 > qw0 + window;
+    }
+    if (active) {
       floatx16 s;
 #pragma unroll
       for (int r = 0; r < 16; ++r) s[r] = 0.f;
@@ -207,6 +232,7 @@ attn_bf16_kernel(const uint16_t *__restrict__ Q, const uint16_t *__restrict__ K,
       for (int ks = 0; ks < NKS; ++ks)
         s = mfma32(as_bf16x8(*reinterpret_cast<const u32x4 *>(sk + krow * D + (((ks * 2 + lhalf) ^ k_swz<D>(krow)) << 3))),
                    qf[ks], s);
+      stream_sched<NKS>();  // keep only a few K fragments live at once
 
       uint32_t vis = 0xffffu;  // bit r: key kbase + 16 (r >> 3) + 8 lhalf + (r & 7)
       if (need_mask) {
@@ -267,14 +293,20 @@ attn_bf16_kernel(const uint16_t *__restrict__ Q, const uint16_t *__restrict__ K,
         const int vrow = db * 32 + lrow;
 #pragma unroll
         for (int h2 = 0; h2 < 2; ++h2)
-          o[db] = mfma32(as_bf16x8(*reinterpret_cast<const u32x4 *>(sv + vt_off(vrow, kb * 4 + 2 * h2 + lhalf))),
-                         pf[h2], o[db]);
+          o[db] = mfma32(as_bf16x8(*reinterpret_cast<const u32x4 *>(sv + vt_off<TK>(vrow, kb * 4 + 2 * h2 + lhalf))), pf[h2],
+                         o[db]);
       }
+      stream_sched<2 * NDB>();
     }
-    // the next tile has landed in every wave's share and every wave is done reading this one
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    };
+    half(0);
+    if constexpr (TK == 64) half(1);
+    // tile kt + 1 has landed in every wave's share (the NSTAGE - 2 younger tiles may stay in flight)
+    // and every wave is done reading tile kt, whose stage the next iteration refills
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"((NSTAGE - 2) * WI) : "memory");
     __syncthreads();
   }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
   lsum += __shfl_xor(lsum, 32, 64);
   if (qi < len) {
