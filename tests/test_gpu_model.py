@@ -113,6 +113,25 @@ def test_9b_shape_two_layers_matches_oracle() -> None:
     _check(probs.cpu().numpy(), w.numpy_weights(), cfg, batch)
 
 
+def test_27b_shape_two_layers_matches_oracle() -> None:
+    """The 27B shape (H 4608, 32/16 heads x 128, query scale 1/sqrt(144), MLP 36864, vocab 256000)
+    through one sliding and one global layer; one request crosses a small window so the sliding
+    mask bites."""
+    import torch
+    from dataclasses import replace
+
+    from deciax_amd import gemma
+
+    say("27b-shaped decision forward, 2 layers, window 128")
+    cfg = replace(gemma.CONFIGS["gemma2-27b"], layers=2, window=128)
+    w = gemma.random_weights(cfg, seed=4, keep_unpacked=True, norm_std=0.3)
+    ids, options = _batch([301, 77], cfg.vocab, 6, seed=9)
+    batch = gemma.pack_batch(ids, options)
+    logits, probs = gemma.forward(w, batch)
+    torch.cuda.synchronize()
+    _check(probs.cpu().numpy(), w.numpy_weights(), cfg, batch)
+
+
 def test_decide_end_to_end() -> None:
     import deciax_amd
 
