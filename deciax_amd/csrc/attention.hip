@@ -110,6 +110,11 @@ DX_DEVICE int k_swz(int row) {
 template <int D>
 constexpr int tile_keys() { return D >= 256 ? 32 : 64; }
 
+template <bool B>
+struct Flag {
+  static constexpr bool value = B;
+};
+
 template <int D, int G, int MODE>
 __global__ void __launch_bounds__(BF_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2)))
 attn_bf16_kernel(const uint16_t *__restrict__ Q, const uint16_t *__restrict__ K, const uint16_t *__restrict__ Vt,
@@ -127,7 +132,7 @@ attn_bf16_kernel(const uint16_t *__restrict__ Q, const uint16_t *__restrict__ K,
   constexpr int NKS = D / 16;
   constexpr int NDB = D / 32;
   constexpr int CPR = D / 8;            // 16-byte chunks per K row
-  static_assert(WI >= 1 && NI % BF_WAVES == 0, "tile too small for the wave count");
+  static_assert(WI >= 2 && WI % 2 == 0 && NI % BF_WAVES == 0, "tile too small for the wave count");
   __shared__ __attribute__((aligned(1024))) uint16_t smem[NSTAGE * STAGE];
 
   const int b = blockIdx.y, g = blockIdx.z;
@@ -163,28 +168,34 @@ attn_bf16_kernel(const uint16_t *__restrict__ Q, const uint16_t *__restrict__ K,
   const int kt0 = klo / TK, kt1 = (khi + TK - 1) / TK;
 
   // K rows past len read as zero (outside the resource); V^T columns stay inside this sequence's
-  // 64-aligned block, whose tail dx_transpose_v zero-fills.
-  const __amdgpu_buffer_rsrc_t rk = make_rsrc(K + start * k_stride + (long)g * D, (long)len * k_stride * 2);
-  const __amdgpu_buffer_rsrc_t rv = make_rsrc(Vt + (long)g * D * vt_ld + vts, ((long)(D - 1) * vt_ld + ((len + 63) & ~63)) * 2);
-  // Instruction i < NI / 2 fills K slots [64 i, 64 i + 64): K row p / CPR, chunk (p % CPR) ^ k_swz(row).
-  // The others fill V^T slots: row p / (TK / 8), chunk (p % (TK / 8)) ^ vt_swz(row). Offsets are
-  // recomputed per issue (a few VALU ops) rather than held in registers.
-  const long ks2 = k_stride * 2, vl2 = vt_ld * 2;
+  // 64-aligned block, whose tail dx_transpose_v zero-fills. Each tile's resources are rebased at the
+  // tile (scalar work), so the per-lane offsets below are loop-invariant.
+  const uint16_t *kbase0 = K + start * k_stride + (long)g * D;
+  const uint16_t *vbase0 = Vt + (long)g * D * vt_ld + vts;
+  const long kbytes = (long)len * k_stride * 2;
+  const long vbytes = ((long)(D - 1) * vt_ld + ((len + 63) & ~63)) * 2;
+  // Wave w fills K instructions [w WI/2, (w + 1) WI/2) and as many V^T instructions. K instruction i
+  // fills K slots [64 i, 64 i + 64): row p / CPR, chunk (p % CPR) ^ k_swz(row); V^T instruction i
+  // fills row p / (TK / 8), chunk (p % (TK / 8)) ^ vt_swz(row).
+  constexpr int WH = WI / 2;
+  int koff[WH], voff[WH];
+#pragma unroll
+  for (int j = 0; j < WH; ++j) {
+    const int p = (wave * WH + j) * 64 + lane;
+    const int krow = p / CPR, kc = (p % CPR) ^ k_swz<D>(krow);
+    koff[j] = (int)(krow * k_stride * 2) + kc * 16;
+    const int vrow = p / (TK / 8), vc = (p % (TK / 8)) ^ vt_swz<TK>(vrow);
+    voff[j] = (int)(vrow * vt_ld * 2) + vc * 16;
+  }
   auto issue = [&](int kt, int st) {
     uint16_t *base = smem + st * STAGE;
+    const long kb = (long)kt * TK;
+    const __amdgpu_buffer_rsrc_t rk = make_rsrc(kbase0 + kb * k_stride, max(kbytes - kb * k_stride * 2, 0L));
+    const __amdgpu_buffer_rsrc_t rv = make_rsrc(vbase0 + kb, vbytes - kb * 2);
 #pragma unroll
-    for (int j = 0; j < WI; ++j) {
-      const int i = wave * WI + j;  // wave-uniform
-      if (i < NI / 2) {
-        const int p = i * 64 + lane;
-        const int krow = p / CPR, kc = (p % CPR) ^ k_swz<D>(krow);
-        // the tile offset goes into the range-checked VGPR offset, so K rows past len read as zero
-        lds_load16(rk, base + i * 512, (int)((kt * TK + krow) * ks2) + kc * 16);
-      } else {
-        const int p = (i - NI / 2) * 64 + lane;
-        const int vrow = p / (TK / 8), vc = (p % (TK / 8)) ^ vt_swz<TK>(vrow);
-        lds_load16(rv, base + KST + (i - NI / 2) * 512, (int)(vrow * vl2) + vc * 16 + kt * TK * 2);
-      }
+    for (int j = 0; j < WH; ++j) {
+      lds_load16(rk, base + (wave * WH + j) * 512, koff[j]);
+      lds_load16(rv, base + KST + (wave * WH + j) * 512, voff[j]);
     }
   };
 
@@ -200,22 +211,10 @@ attn_bf16_kernel(const uint16_t *__restrict__ Q, const uint16_t *__restrict__ K,
   const float c2 = -2.f * LOG2E * softcap;
   const float c3 = 0.5f * LOG2E * softcap;
 
-  // Ring of NSTAGE tiles: tile kt sits in stage (kt - kt0) % NSTAGE, and tile kt + NSTAGE - 1 is
-  // fetched while tile kt is multiplied (clamped: the last tiles reload themselves harmlessly).
-#pragma unroll
-  for (int i = 0; i < NSTAGE - 1; ++i) issue(min(kt0 + i, kt1 - 1), i);
-  asm volatile("s_waitcnt vmcnt(%0)" ::"n"((NSTAGE - 2) * WI) : "memory");
-  __syncthreads();
-  for (int kt = kt0; kt < kt1; ++kt) {
-    const int st = (kt - kt0) % NSTAGE;
-    issue(min(kt + NSTAGE - 1, kt1 - 1), (kt - kt0 + NSTAGE - 1) % NSTAGE);
-    const uint16_t *sk = smem + st * STAGE;
-    const uint16_t *sv = sk + KST;
-    auto half = [&](const int kb) {
-    const int kbase = kt * TK + kb * 32;
-
+  // Which 32-key blocks this wave's rows see: active = some key visible, masked = some key hidden.
+  auto block_state = [&](const int kbase, bool &need_mask) {
     bool active = qw0 < len;
-    bool need_mask = kbase + 32 > len;
+    need_mask = kbase + 32 > len;
     if (causal) {
       active = active && kbase <= qw1 && !(window > 0 && kbase + 31 <= qw0 - window);
       need_mask = need_mask || kbase + 31 > qw0 || (window > 0 && kbase <= qw1 - window);
@@ -223,88 +222,145 @@ attn_bf16_kernel(const uint16_t *__restrict__ Q, const uint16_t *__restrict__ K,
       active = active && kbase <= qw1 + window && kbase + 31 >= qw0 - window;
       need_mask = need_mask || kbase < qw1 - window || kbase + 31 > qw0 + window;
     }
-    if (active) {
-      floatx16 s;
+    return active;
+  };
+  // Visible keys of row qi form one interval [vlo, vhi].
+  int vlo, vhi;
+  if (causal) {
+    vhi = min(qi, len - 1);
+    vlo = window > 0 ? qi - window + 1 : 0;
+  } else {
+    vhi = window > 0 ? min(qi + window, len - 1) : len - 1;
+    vlo = window > 0 ? qi - window : 0;
+  }
+
+  // One 32-key block kb of the tile in stage sk (K, then V^T at sk + KST): S^T = K Q^T, softmax,
+  // O^T += V^T P^T. MASKED evaluates the causal / window / length mask and skips blocks no row sees.
+  auto block = [&](const uint16_t *sk, const int kbase, const int kb, auto masked) {
+    constexpr bool M = decltype(masked)::value;
+    if constexpr (M) {
+      bool need_mask;
+      if (!block_state(kbase, need_mask)) return;
+    }
+    floatx16 s;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) s[r] = 0.f;
+    for (int r = 0; r < 16; ++r) s[r] = 0.f;
+    {
+      // for ks and ks + 8 the swizzled slots differ by the same 16 chunks: 8 lane offsets serve all 16
       const int krow = kb * 32 + kperm(lrow);
 #pragma unroll
-      for (int ks = 0; ks < NKS; ++ks)
-        s = mfma32(as_bf16x8(*reinterpret_cast<const u32x4 *>(sk + krow * D + (((ks * 2 + lhalf) ^ k_swz<D>(krow)) << 3))),
-                   qf[ks], s);
+      for (int ks = 0; ks < NKS; ++ks) {
+        const int lo = (((ks & 7) * 2 + lhalf) ^ k_swz<D>(krow)) << 3;
+        s = mfma32(as_bf16x8(*reinterpret_cast<const u32x4 *>(sk + krow * D + (ks & ~7) * 16 + lo)), qf[ks], s);
+      }
       stream_sched<NKS>();  // keep only a few K fragments live at once
-
-      uint32_t vis = 0xffffu;  // bit r: key kbase + 16 (r >> 3) + 8 lhalf + (r & 7)
-      if (need_mask) {
-        vis = 0;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int key = kbase + 16 * (r >> 3) + 8 * lhalf + (r & 7);
-          vis |= (uint32_t)visible(qi, key, len, window, causal) << r;
-        }
-      }
-
-      if constexpr (MODE == MODE_FIXED) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const float e = fast_exp2(s[r] * c1);
-          const float p = fast_exp2(c3 + c2 * fast_rcp(1.f + e));
-          s[r] = ((vis >> r) & 1u) ? p : 0.f;
-          lsum += s[r];
-        }
-      } else {
-        float tmax = NEG_BIG;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          float t = s[r] * scale;
-          if (softcap > 0.f) t = softcap * tanhf(t / softcap);
-          t *= LOG2E;
-          t = ((vis >> r) & 1u) ? t : NEG_BIG;
-          s[r] = t;
-          tmax = fmaxf(tmax, t);
-        }
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-        const float mnew = fmaxf(mrun, tmax);
-        const float alpha = fast_exp2(mrun - mnew);
-        mrun = mnew;
-        lsum *= alpha;
-#pragma unroll
-        for (int i = 0; i < NDB; ++i)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) o[i][r] *= alpha;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const float p = ((vis >> r) & 1u) ? fast_exp2(s[r] - mnew) : 0.f;
-          s[r] = p;
-          lsum += p;
-        }
-      }
-
-      bf16x8 pf[2];
-#pragma unroll
-      for (int h2 = 0; h2 < 2; ++h2) {
-        u32x4 w;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) w[i] = pack_bf2(s[8 * h2 + 2 * i], s[8 * h2 + 2 * i + 1]);
-        pf[h2] = as_bf16x8(w);
-      }
-#pragma unroll
-      for (int db = 0; db < NDB; ++db) {
-        const int vrow = db * 32 + lrow;
-#pragma unroll
-        for (int h2 = 0; h2 < 2; ++h2)
-          o[db] = mfma32(as_bf16x8(*reinterpret_cast<const u32x4 *>(sv + vt_off<TK>(vrow, kb * 4 + 2 * h2 + lhalf))), pf[h2],
-                         o[db]);
-      }
-      stream_sched<2 * NDB>();
     }
-    };
-    half(0);
-    if constexpr (TK == 64) half(1);
+    // key of score r: kbase + 16 (r >> 3) + 8 lhalf + (r & 7); visible iff inside [vlo, vhi]
+    const int mlo = vlo - kbase - 8 * lhalf, mhi = vhi - kbase - 8 * lhalf;
+    auto keep = [&](int r) { return 16 * (r >> 3) + (r & 7) >= mlo && 16 * (r >> 3) + (r & 7) <= mhi; };
+    if constexpr (MODE == MODE_FIXED) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float e = fast_exp2(s[r] * c1);
+        float p = fast_exp2(c3 + c2 * fast_rcp(1.f + e));
+        if constexpr (M) p = keep(r) ? p : 0.f;
+        s[r] = p;
+        lsum += p;
+      }
+    } else {
+      float tmax = NEG_BIG;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        float t = s[r] * scale;
+        if (softcap > 0.f) t = softcap * tanhf(t / softcap);
+        t *= LOG2E;
+        if constexpr (M) t = keep(r) ? t : NEG_BIG;
+        s[r] = t;
+        tmax = fmaxf(tmax, t);
+      }
+      tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+      const float mnew = fmaxf(mrun, tmax);
+      const float alpha = fast_exp2(mrun - mnew);
+      mrun = mnew;
+      lsum *= alpha;
+#pragma unroll
+      for (int i = 0; i < NDB; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[i][r] *= alpha;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        float p = fast_exp2(s[r] - mnew);
+        if constexpr (M) p = keep(r) ? p : 0.f;
+        s[r] = p;
+        lsum += p;
+      }
+    }
+    bf16x8 pf[2];
+#pragma unroll
+    for (int h2 = 0; h2 < 2; ++h2) {
+      u32x4 w;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) w[i] = pack_bf2(s[8 * h2 + 2 * i], s[8 * h2 + 2 * i + 1]);
+      pf[h2] = as_bf16x8(w);
+    }
+    const uint16_t *sv = sk + KST;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) {
+      const int vrow = db * 32 + lrow;
+#pragma unroll
+      for (int h2 = 0; h2 < 2; ++h2)
+        o[db] = mfma32(as_bf16x8(*reinterpret_cast<const u32x4 *>(sv + vt_off<TK>(vrow, kb * 4 + 2 * h2 + lhalf))),
+                       pf[h2], o[db]);
+    }
+    stream_sched<2 * NDB>();
+  };
+
+  // Ring of NSTAGE tiles: tile kt sits in stage (kt - kt0) % NSTAGE, and tile kt + NSTAGE - 1 is
+  // fetched while tile kt is multiplied (clamped: the last tiles reload themselves harmlessly).
+  auto tile = [&](const int kt, auto masked) {
+    issue(min(kt + NSTAGE - 1, kt1 - 1), (kt - kt0 + NSTAGE - 1) % NSTAGE);
+    const uint16_t *sk = smem + ((kt - kt0) % NSTAGE) * STAGE;
+#pragma unroll
+    for (int kb = 0; kb < TK / 32; ++kb) block(sk, kt * TK + kb * 32, kb, masked);
     // tile kt + 1 has landed in every wave's share (the NSTAGE - 2 younger tiles may stay in flight)
     // and every wave is done reading tile kt, whose stage the next iteration refills
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"((NSTAGE - 2) * WI) : "memory");
     __syncthreads();
+  };
+
+  // Tiles [ta, tb) hold no key this wave's rows cannot see (all blocks active, none masked): they run
+  // without any mask code. The tiles before and after take the masked body. Every wave runs one
+  // iteration (one barrier) per tile, whichever body.
+  int ta = kt1, tb = kt1;
+  if (qw1 < len) {
+    int lo_u = 0, hi_u = len - 32;  // first / last kbase of an unmasked block
+    if (causal) {
+      hi_u = min(hi_u, qw0 - 31);
+      if (window > 0) lo_u = qw1 - window + 1;
+    } else if (window > 0) {
+      lo_u = qw1 - window;
+      hi_u = min(hi_u, qw0 + window - 31);
+    }
+    lo_u = max(lo_u, 0);
+    const int a = max(kt0, (lo_u + TK - 1) / TK);
+    const int last = hi_u - (TK - 32);  // kbase of the tile's first block
+    const int b = last < 0 ? kt0 : min(kt1, last / TK + 1);
+    if (a < b) {
+      ta = a;
+      tb = b;
+    }
+  }
+
+#pragma unroll
+  for (int i = 0; i < NSTAGE - 1; ++i) issue(min(kt0 + i, kt1 - 1), i);
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"((NSTAGE - 2) * WI) : "memory");
+  __syncthreads();
+  for (int kt = kt0; kt < kt1; ++kt) {
+    if (kt == ta) {
+      for (; kt < tb; ++kt) tile(kt, Flag<false>());
+      if (kt == kt1) break;
+    }
+    tile(kt, Flag<true>());
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 

@@ -30,7 +30,10 @@ DX_DEVICE float round_bf(float f) { return bf2f(f2bf(f)); }
 
 // Two fp32 values -> one dword of two bf16 (lo in the low half).
 DX_DEVICE uint32_t pack_bf2(float lo, float hi) {
-  return (uint32_t)f2bf(lo) | ((uint32_t)f2bf(hi) << 16);
+  typedef float floatx2 __attribute__((ext_vector_type(2)));
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  const floatx2 v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));  // one v_cvt_pk_bf16_f32
 }
 
 DX_DEVICE float lo_bf(uint32_t w) { return __uint_as_float(w << 16); }
