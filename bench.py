@@ -96,8 +96,8 @@ class KernelTimer:
         wrap("gated_linear", lambda a, k: "gate_up_proj")
         wrap("attention_vt", lambda a, k: "attention_sliding" if k.get("window", 0) else "attention_global")
         wrap("add_rmsnorm", lambda a, k: "add_rmsnorm")
-        wrap("rope", lambda a, k: "rope")
-        wrap("transpose_v", lambda a, k: "transpose_v")
+        wrap("qkv_rope", lambda a, k: "qkv_proj")
+        wrap("vt_zero_tails", lambda a, k: "vt_zero_tails")
         wrap("embed", lambda a, k: "embed")
         wrap("readout", lambda a, k: "readout")
 

@@ -44,8 +44,14 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
          c_float, c_float, c_int32, c_int32, _p],
     ),
     "dx_transpose_v": (c_int, [_p, _p, _p, _p, _p, c_int32, c_int32, c_int32, c_int32, c_int64, c_int64, _p]),
+    "dx_vt_zero_tails": (c_int, [_p, _p, _p, c_int32, c_int32, c_int64, _p]),
     "dx_linear": (c_int, [_p, _p, _p, c_int64, c_int64, c_int64, c_int64, c_int64, c_int64, c_int32, _p]),
     "dx_gated_linear": (c_int, [_p, _p, _p, c_int64, c_int64, c_int64, c_int64, c_int64, c_int32, _p]),
+    "dx_qkv_rope": (
+        c_int,
+        [_p, _p, _p, _p, _p, _p, _p, _p, c_int64, c_int64, c_int32, c_int32, c_int32, c_int64, c_int64, c_int64,
+         c_int32, _p],
+    ),
     "dx_pack_gate_up": (c_int, [_p, _p, _p, c_int64, c_int64, _p]),
     "dx_norm_project": (
         c_int, [_p, _p, _p, _p, _p, c_int64, c_int64, c_int64, c_float, _p, c_int64, _p]),

@@ -156,6 +156,50 @@ int dx_transpose_v(const void *v, void *vt, const int32_t *seq_start, const int3
                       "transpose_v launch");
 }
 
+int dx_vt_zero_tails(void *vt, const int32_t *seq_len, const int32_t *vt_start, int32_t num_seqs, int32_t vt_rows,
+                     int64_t vt_ld, void *stream) {
+  REQUIRE(vt && seq_len && vt_start, "vt_zero_tails: null pointer argument");
+  REQUIRE(num_seqs >= 0 && vt_rows >= 0 && vt_ld > 0 && vt_ld % 8 == 0, "vt_zero_tails: bad sizes");
+  if (num_seqs == 0 || vt_rows == 0) return DX_OK;
+  return check_launch(dx_vt_zero_tails_launch(static_cast<uint16_t *>(vt), seq_len, vt_start, num_seqs, vt_rows,
+                                              vt_ld, as_stream(stream)),
+                      "vt_zero_tails launch");
+}
+
+int dx_qkv_rope(const void *x, const void *w_qkv, void *qk, void *vt, const int32_t *positions, const int32_t *vt_col,
+                const void *cos, const void *sin, int64_t rows, int64_t hidden, int32_t num_q_heads,
+                int32_t num_kv_heads, int32_t head_dim, int64_t ldx, int64_t ld_qk, int64_t vt_ld, int32_t max_pos,
+                void *stream) {
+  REQUIRE(x && w_qkv && qk && vt && positions && vt_col && cos && sin, "qkv_rope: null pointer argument");
+  REQUIRE(rows >= 0 && hidden > 0 && num_q_heads > 0 && num_kv_heads > 0 && max_pos > 0, "qkv_rope: bad sizes");
+  SUPPORTED(head_dim == 64 || head_dim == 128 || head_dim == 256, "qkv_rope: head_dim %d not in {64, 128, 256}",
+            head_dim);
+  const int64_t qk_cols = (int64_t)(num_q_heads + num_kv_heads) * head_dim;
+  const int64_t n = qk_cols + (int64_t)num_kv_heads * head_dim;
+  SUPPORTED(n % 256 == 0, "qkv_rope: packed width %ld must be a multiple of 256", (long)n);
+  SUPPORTED(hidden % 64 == 0, "qkv_rope: hidden=%ld must be a multiple of 64", (long)hidden);
+  REQUIRE(ldx >= hidden && ldx % 8 == 0 && ld_qk >= qk_cols && ld_qk % 8 == 0 && vt_ld > 0,
+          "qkv_rope: leading dimensions must cover the row and be multiples of 8");
+  SUPPORTED(ldx <= DX_MAX_LD && hidden <= DX_MAX_LD, "qkv_rope: leading dimensions above %d", DX_MAX_LD);
+  REQUIRE(aligned16(x) && aligned16(w_qkv) && aligned16(qk) && aligned16(cos) && aligned16(sin),
+          "qkv_rope: pointers must be 16-byte aligned");
+  if (rows == 0) return DX_OK;
+  QkvEpilogue qe;
+  qe.vt = static_cast<uint16_t *>(vt);
+  qe.vt_col = vt_col;
+  qe.pos = positions;
+  qe.cos = static_cast<const uint16_t *>(cos);
+  qe.sin = static_cast<const uint16_t *>(sin);
+  qe.vt_ld = vt_ld;
+  qe.qk_cols = (int)qk_cols;
+  qe.d = head_dim;
+  qe.max_pos = max_pos;
+  return check_launch(dx_gemm_qkv(static_cast<const uint16_t *>(x), static_cast<const uint16_t *>(w_qkv),
+                                  static_cast<uint16_t *>(qk), rows, n, hidden, ldx, hidden, ld_qk, qe,
+                                  as_stream(stream)),
+                      "qkv_rope launch");
+}
+
 int dx_linear(const void *x, const void *w, void *y, int64_t m, int64_t n, int64_t k, int64_t ldx, int64_t ldw,
               int64_t ldy, int32_t out_dtype, void *stream) {
   REQUIRE(x && w && y, "linear: null pointer argument");

@@ -516,6 +516,15 @@ transpose_v_kernel(const uint16_t *__restrict__ V, uint16_t *__restrict__ Vt, co
   }
 }
 
+// Block (s, y): V^T rows [4 y, 4 y + 4) of sequence s, columns [seq_len, seq_len rounded up to 64) <- 0.
+__global__ void __launch_bounds__(THREADS)
+vt_zero_tails_kernel(uint16_t *__restrict__ Vt, const int32_t *__restrict__ seq_len,
+                     const int32_t *__restrict__ vt_start, int vt_rows, long vt_ld) {
+  const int len = max(seq_len[blockIdx.x], 0);
+  const int row = blockIdx.y * (THREADS / 64) + (int)threadIdx.x / 64, j = len + (int)threadIdx.x % 64;
+  if (row < vt_rows && j < ((len + 63) & ~63)) Vt[(long)row * vt_ld + vt_start[blockIdx.x] + j] = 0;
+}
+
 template <int D, int G>
 hipError_t launch_bf16_dg(const AttnArgs &a, hipStream_t s) {
   constexpr int BQ = 32 * (BF_WAVES / G);
@@ -568,6 +577,13 @@ hipError_t dx_attn_f32(const AttnArgs &a, hipStream_t s) {
     case 256: return launch_f32_d<256, 4>(a, s);
   }
   return hipErrorInvalidValue;
+}
+
+hipError_t dx_vt_zero_tails_launch(uint16_t *vt, const int32_t *seq_len, const int32_t *vt_start, int num_seqs,
+                                   int vt_rows, long vt_ld, hipStream_t s) {
+  const dim3 grid((unsigned)num_seqs, (unsigned)((vt_rows + THREADS / 64 - 1) / (THREADS / 64)));
+  vt_zero_tails_kernel<<<grid, dim3(THREADS), 0, s>>>(vt, seq_len, vt_start, vt_rows, vt_ld);
+  return hipGetLastError();
 }
 
 hipError_t dx_transpose_v_launch(const uint16_t *v, uint16_t *vt, const int32_t *seq_start, const int32_t *seq_len,

@@ -26,7 +26,12 @@
 // store, and the gated activation for a gate|up weight packed in 64-row
 // blocks (dx_pack_gate_up), which writes act = bf16(bf16(act(g)) * u) with
 // g, u rounded to bf16 first — the rounding points of the reference's fused
-// MLP epilogue (src/deciax/kernels/swiglu.py:100-101).
+// MLP epilogue (src/deciax/kernels/swiglu.py:100-101). The QKV epilogue
+// (q | k | v packed weight) applies rotate-half RoPE to the q and k heads of the
+// tile with the rounding of dx_rope (the RoPE-in-projection pattern of
+// src/deciax/kernels/fused.py:93-99,120-122 on the formula of
+// src/deciax/nn.py:35-44), and scatters v transposed into V^T, the layout the
+// attention kernel stages (one column per token: vt_col[row]).
 #include "common.h"
 #include "kernels.h"
 
@@ -36,7 +41,7 @@ constexpr int BK = 64;
 constexpr int BN = 256;
 constexpr int THREADS = 256;
 
-enum { EPI_BF16 = 0, EPI_F32 = 1, EPI_GATED = 2 };
+enum { EPI_BF16 = 0, EPI_F32 = 1, EPI_GATED = 2, EPI_QKV = 3 };
 
 // Workgroups are dispatched round-robin over the 8 XCDs (each with its own
 // L2). Renumber so each XCD gets a contiguous run of logical tiles, then walk
@@ -65,7 +70,7 @@ DX_DEVICE __amdgpu_buffer_rsrc_t make_rsrc(const uint16_t *base, long bytes) {
 template <int BM, int EPI>
 __global__ void __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(1, 1)))
 gemm_nt_kernel(const uint16_t *__restrict__ A, const uint16_t *__restrict__ B, void *__restrict__ C, int M, int N,
-               int K, long lda, long ldb, long ldc, int act) {
+               int K, long lda, long ldb, long ldc, int act, QkvEpilogue qe) {
   constexpr int TM = BM / 64, TN = BN / 64;  // 32x32 blocks per wave along m, n
   constexpr int STAGE = (BM + BN) * BK;
   constexpr int AC = BM * BK / 8 / THREADS, BC = BN * BK / 8 / THREADS;  // 16-byte chunks per thread
@@ -216,7 +221,7 @@ gemm_nt_kernel(const uint16_t *__restrict__ A, const uint16_t *__restrict__ B, v
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int row = wm * (BM / 2) + i * 32 + (r >> 2) * 8 + lhalf * 4 + (r & 3);
-        if constexpr (EPI == EPI_BF16) {
+        if constexpr (EPI == EPI_BF16 || EPI == EPI_QKV) {
 #pragma unroll
           for (int j = 0; j < TN; ++j) {
             const int col = wn * (BN / 2) + j * 32 + lrow;
@@ -236,32 +241,74 @@ gemm_nt_kernel(const uint16_t *__restrict__ A, const uint16_t *__restrict__ B, v
       }
     __syncthreads();
     uint16_t *Cb = reinterpret_cast<uint16_t *>(C);
-    const int out_n0 = EPI == EPI_GATED ? n0 / 2 : n0;
-    constexpr int CPR = OUT_W / 8;  // 16-byte chunks per row
-    for (int idx = tid; idx < BM * CPR; idx += THREADS) {
-      const int row = idx / CPR, c = idx % CPR;
-      if (m0 + row < M)
-        *reinterpret_cast<u32x4 *>(Cb + (long)(m0 + row) * ldc + out_n0 + c * 8) =
-            *reinterpret_cast<const u32x4 *>(smem + row * OUT_PITCH + c * 8);
+    if constexpr (EPI == EPI_QKV) {
+      // q / k heads (head columns below qk_cols): item = (row, head, 8 rotary pairs j0..j0+7)
+      const int d = qe.d, half = d / 2, per_head = d / 16;
+      for (int idx = tid; idx < BM * (BN / 16); idx += THREADS) {
+        const int row = idx / (BN / 16), rem = idx % (BN / 16);
+        const int j0 = (rem % per_head) * 8, c1 = (rem / per_head) * d + j0;
+        if (m0 + row >= M || n0 + c1 >= qe.qk_cols) continue;
+        const int p = min(max(qe.pos[m0 + row], 0), qe.max_pos - 1);
+        const u32x4 a = *reinterpret_cast<const u32x4 *>(smem + row * OUT_PITCH + c1);
+        const u32x4 b = *reinterpret_cast<const u32x4 *>(smem + row * OUT_PITCH + c1 + half);
+        const u32x4 cs = *reinterpret_cast<const u32x4 *>(qe.cos + (long)p * half + j0);
+        const u32x4 sn = *reinterpret_cast<const u32x4 *>(qe.sin + (long)p * half + j0);
+        u32x4 o1, o2;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          float r1[2], r2[2];
+          const float av[2] = {lo_bf(a[j]), hi_bf(a[j])}, bv[2] = {lo_bf(b[j]), hi_bf(b[j])};
+          const float cv[2] = {lo_bf(cs[j]), hi_bf(cs[j])}, sv[2] = {lo_bf(sn[j]), hi_bf(sn[j])};
+#pragma unroll
+          for (int e = 0; e < 2; ++e) {
+            r1[e] = round_bf(av[e] * cv[e]) - round_bf(bv[e] * sv[e]);
+            r2[e] = round_bf(bv[e] * cv[e]) + round_bf(av[e] * sv[e]);
+          }
+          o1[j] = pack_bf2(r1[0], r1[1]);
+          o2[j] = pack_bf2(r2[0], r2[1]);
+        }
+        uint16_t *dst = Cb + (long)(m0 + row) * ldc + n0 + c1;
+        *reinterpret_cast<u32x4 *>(dst) = o1;
+        *reinterpret_cast<u32x4 *>(dst + half) = o2;
+      }
+      // v (columns from qk_cols on): tile column c is V^T row n0 + c - qk_cols. A thread keeps one
+      // row (token), so the lanes of a store instruction write consecutive V^T columns.
+      if (n0 + BN > qe.qk_cols) {
+        const int row = tid % BM;
+        if (m0 + row < M) {
+          const long col = qe.vt_col[m0 + row];
+          for (int c = max(qe.qk_cols - n0, 0) + tid / BM; c < BN; c += THREADS / BM)
+            qe.vt[(long)(n0 + c - qe.qk_cols) * qe.vt_ld + col] = smem[row * OUT_PITCH + c];
+        }
+      }
+    } else {
+      const int out_n0 = EPI == EPI_GATED ? n0 / 2 : n0;
+      constexpr int CPR = OUT_W / 8;  // 16-byte chunks per row
+      for (int idx = tid; idx < BM * CPR; idx += THREADS) {
+        const int row = idx / CPR, c = idx % CPR;
+        if (m0 + row < M)
+          *reinterpret_cast<u32x4 *>(Cb + (long)(m0 + row) * ldc + out_n0 + c * 8) =
+              *reinterpret_cast<const u32x4 *>(smem + row * OUT_PITCH + c * 8);
+      }
     }
   }
 }
 
 template <int BM, int EPI>
 hipError_t launch(const uint16_t *A, const uint16_t *B, void *C, long M, long N, long K, long lda, long ldb,
-                  long ldc, int act, hipStream_t s) {
+                  long ldc, int act, const QkvEpilogue &qe, hipStream_t s) {
   const long num_m = (M + BM - 1) / BM, num_n = N / BN;
   gemm_nt_kernel<BM, EPI><<<dim3((unsigned)(num_m * num_n)), dim3(THREADS), 0, s>>>(
-      A, B, C, (int)M, (int)N, (int)K, lda, ldb, ldc, act);
+      A, B, C, (int)M, (int)N, (int)K, lda, ldb, ldc, act, qe);
   return hipGetLastError();
 }
 
 template <int EPI>
 hipError_t dispatch(const uint16_t *A, const uint16_t *B, void *C, long M, long N, long K, long lda, long ldb,
-                    long ldc, int act, hipStream_t s) {
+                    long ldc, int act, hipStream_t s, const QkvEpilogue &qe = QkvEpilogue{}) {
   // Small M: halve the row tile so more workgroups exist.
-  if (M <= 1024) return launch<128, EPI>(A, B, C, M, N, K, lda, ldb, ldc, act, s);
-  return launch<256, EPI>(A, B, C, M, N, K, lda, ldb, ldc, act, s);
+  if (M <= 1024) return launch<128, EPI>(A, B, C, M, N, K, lda, ldb, ldc, act, qe, s);
+  return launch<256, EPI>(A, B, C, M, N, K, lda, ldb, ldc, act, qe, s);
 }
 
 }  // namespace
@@ -279,4 +326,9 @@ hipError_t dx_gemm_f32(const uint16_t *A, const uint16_t *B, float *C, long M, l
 hipError_t dx_gemm_gated(const uint16_t *A, const uint16_t *B, uint16_t *C, long M, long F, long K, long lda,
                          long ldc, int act, hipStream_t s) {
   return dispatch<EPI_GATED>(A, B, C, M, 2 * F, K, lda, K, ldc, act, s);
+}
+
+hipError_t dx_gemm_qkv(const uint16_t *A, const uint16_t *B, uint16_t *QK, long M, long N, long K, long lda, long ldb,
+                       long ld_qk, const QkvEpilogue &qe, hipStream_t s) {
+  return dispatch<EPI_QKV>(A, B, QK, M, N, K, lda, ldb, ld_qk, 0, s, qe);
 }

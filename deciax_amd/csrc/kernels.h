@@ -16,6 +16,22 @@ hipError_t dx_gemm_f32(const uint16_t *A, const uint16_t *B, float *C, long M, l
 hipError_t dx_gemm_gated(const uint16_t *A, const uint16_t *B, uint16_t *C, long M, long F, long K, long lda,
                          long ldc, int act, hipStream_t s);
 
+// QKV epilogue parameters: columns [0, qk_cols) of the packed projection are q | k heads of size d
+// (RoPE with bf16 cos/sin tables [max_pos, d / 2] at pos[row]); columns [qk_cols, N) are v, written to
+// vt[(col - qk_cols) * vt_ld + vt_col[row]].
+struct QkvEpilogue {
+  uint16_t *vt = nullptr;
+  const int32_t *vt_col = nullptr;
+  const int32_t *pos = nullptr;
+  const uint16_t *cos = nullptr, *sin = nullptr;
+  long vt_ld = 0;
+  int qk_cols = 0, d = 0, max_pos = 0;
+};
+hipError_t dx_gemm_qkv(const uint16_t *A, const uint16_t *B, uint16_t *QK, long M, long N, long K, long lda, long ldb,
+                       long ld_qk, const QkvEpilogue &qe, hipStream_t s);
+hipError_t dx_vt_zero_tails_launch(uint16_t *vt, const int32_t *seq_len, const int32_t *vt_start, int num_seqs,
+                                   int vt_rows, long vt_ld, hipStream_t s);
+
 struct AttnArgs {
   const void *q, *k, *v;  // v: token-major (fp32 path) or transposed (bf16 path)
   void *out;

@@ -5,10 +5,10 @@ embedding gather, L decoder layers, final norm, option head — with each step a
 call into the gfx950 kernels:
 
     embed (+ layer-0 input norm)                      dx_embed
+    zero the V^T tail of each sequence (once)         dx_vt_zero_tails
     per layer:
-      qkv = h @ Wqkv^T  (q|k|v packed, one GEMM)       dx_linear
-      RoPE on the q and k heads, in place              dx_rope
-      V -> V^T per sequence                            dx_transpose_v
+      q|k|v = h @ Wqkv^T (one GEMM), RoPE on q and k   dx_qkv_rope
+        in the epilogue, V written transposed (V^T)
       causal GQA flash attention, softcap 50,          dx_attn_prefill_vt
         sliding window 4096 on even layers
       y = att @ Wo^T                                   dx_linear
@@ -285,6 +285,7 @@ class PackedBatch:
     seq_len: torch.Tensor
     vt_start: torch.Tensor
     vt_ld: int
+    vt_col: torch.Tensor  # per row: vt_start of its sequence + its position (its V^T column)
     opt_pos: torch.Tensor
     opt_label: torch.Tensor
     q_offsets: torch.Tensor
@@ -327,8 +328,9 @@ def pack_batch(token_ids: Sequence[Sequence[int]], options: Sequence[Sequence[Se
     def i32(a: Sequence[int] | np.ndarray) -> torch.Tensor:
         return torch.as_tensor(np.asarray(a, dtype=np.int64).astype(np.int32)).to(dev)
 
+    vt_col = np.repeat(vt_start, lengths) + positions
     return PackedBatch(lengths, i32(ids), i32(positions), i32(starts), i32(lengths), i32(vt_start),
-                       int(sum(padded)), i32(opt_pos), i32(opt_label), i32(q_off), qpr, opq)
+                       int(sum(padded)), i32(vt_col), i32(opt_pos), i32(opt_label), i32(q_off), qpr, opq)
 
 
 class Workspace:
@@ -362,11 +364,9 @@ def layer_forward(w: DecisionWeights, i: int, batch: PackedBatch, ws: Workspace)
     x, h, y = ws.x[:rows], ws.h[:rows], ws.y[:rows]
     qkv, att, act = ws.qkv[:rows], ws.att[:rows], ws.act[:rows]
     qd, kd = c.heads * c.head_dim, c.kv_heads * c.head_dim
-    K.linear(h, lw.qkv, out=qkv)
-    K.rope(qkv, batch.positions, w.cos, w.sin, num_heads=c.heads + c.kv_heads, head_dim=c.head_dim)
     vt = ws.vt[:, :batch.vt_ld]
-    K.transpose_v(qkv[:, qd + kd:], vt, batch.seq_start, batch.seq_len, batch.vt_start, batch.max_len,
-                  num_kv_heads=c.kv_heads, head_dim=c.head_dim)
+    K.qkv_rope(h, lw.qkv, qkv, vt, batch.positions, batch.vt_col, w.cos, w.sin, num_q_heads=c.heads,
+               num_kv_heads=c.kv_heads, head_dim=c.head_dim)
     K.attention_vt(qkv[:, :qd], qkv[:, qd:qd + kd], vt, batch.seq_start, batch.seq_len, batch.vt_start,
                    batch.max_len, num_q_heads=c.heads, num_kv_heads=c.kv_heads, head_dim=c.head_dim,
                    scale=c.query_scale, softcap=c.attn_softcap, window=c.window if c.sliding(i) else 0,
@@ -390,6 +390,7 @@ def forward(w: DecisionWeights, batch: PackedBatch, ws: Workspace | None = None,
     rows = batch.rows
     x, h = ws.x[:rows], ws.h[:rows]
     K.embed(batch.ids, w.embed, scale=embed_scale(c.hidden), norm_w=w.layers[0].input_norm, eps=c.eps, x=x, h=h)
+    K.vt_zero_tails(ws.vt[:, :batch.vt_ld], batch.seq_len, batch.vt_start)
     n = c.layers if layers is None else layers
     for i in range(n):
         layer_forward(w, i, batch, ws)

@@ -81,6 +81,32 @@ def linear(x: torch.Tensor, w: torch.Tensor, *, out: torch.Tensor | None = None,
     return out
 
 
+def qkv_rope(x: torch.Tensor, w_qkv: torch.Tensor, qk: torch.Tensor, vt: torch.Tensor, positions: torch.Tensor,
+             vt_col: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, *, num_q_heads: int, num_kv_heads: int,
+             head_dim: int) -> torch.Tensor:
+    """Packed q | k | v projection with RoPE on q and k in the epilogue (`fused.py:93-99,120-122`):
+    qk [rows, >= (Hq + Hkv) D] receives rotated q | k; V goes transposed into vt at column vt_col[row]
+    (the layout of `attention_vt`; columns past each sequence's length are left to `vt_zero_tails`)."""
+    for t, n in ((x, "x"), (w_qkv, "w_qkv"), (qk, "qk"), (vt, "vt"), (cos, "cos"), (sin, "sin")):
+        _need(t, n, BF16, 2)
+    _need(positions, "positions", torch.int32, 1)
+    _need(vt_col, "vt_col", torch.int32, 1)
+    rows, hidden = x.shape
+    width = (num_q_heads + 2 * num_kv_heads) * head_dim
+    if w_qkv.shape != (width, hidden):
+        raise ValueError(f"qkv_rope: weight must be [{width}, {hidden}], got {tuple(w_qkv.shape)}")
+    if qk.shape[0] < rows or vt.shape[0] != num_kv_heads * head_dim:
+        raise ValueError("qkv_rope: qk needs a row per token and vt one row per (kv head, dim)")
+    if positions.shape[0] != rows or vt_col.shape[0] != rows:
+        raise ValueError("qkv_rope: one position and one V^T column per row")
+    if cos.shape != sin.shape or cos.shape[1] != head_dim // 2:
+        raise ValueError("qkv_rope: cos/sin tables must be [max_pos, head_dim / 2]")
+    call("dx_qkv_rope", _ptr(x), _ptr(w_qkv), _ptr(qk), _ptr(vt), _ptr(positions), _ptr(vt_col), _ptr(cos), _ptr(sin),
+         rows, hidden, num_q_heads, num_kv_heads, head_dim, _rows(x, "x"), _rows(qk, "qk"), _rows(vt, "vt"),
+         cos.shape[0], _stream())
+    return qk
+
+
 def pack_gate_up(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
     """[f, k] gate and up weights -> the [2f, k] packed layout of `gated_linear`
     (the role of `pack`, src/deciax/kernels/swiglu.py:45-51)."""
@@ -265,6 +291,18 @@ def transpose_v(v: torch.Tensor, vt: torch.Tensor, seq_start: torch.Tensor, seq_
     _need(vt, "vt", BF16, 2)
     call("dx_transpose_v", _ptr(v), _ptr(vt), _ptr(seq_start), _ptr(seq_len), _ptr(vt_start), seq_start.shape[0],
          max_seq_len, num_kv_heads, head_dim, _rows(v, "v"), _rows(vt, "vt"), _stream())
+    return vt
+
+
+def vt_zero_tails(vt: torch.Tensor, seq_len: torch.Tensor, vt_start: torch.Tensor) -> torch.Tensor:
+    """Zero each sequence's V^T columns past its length, up to the next multiple of 64."""
+    _need(vt, "vt", BF16, 2)
+    _need(seq_len, "seq_len", torch.int32, 1)
+    _need(vt_start, "vt_start", torch.int32, 1)
+    if seq_len.shape != vt_start.shape:
+        raise ValueError("vt_zero_tails: one vt_start per sequence")
+    call("dx_vt_zero_tails", _ptr(vt), _ptr(seq_len), _ptr(vt_start), seq_len.shape[0], vt.shape[0],
+         _rows(vt, "vt"), _stream())
     return vt
 
 

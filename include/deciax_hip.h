@@ -116,6 +116,17 @@ int dx_transpose_v(const void *v, void *vt, const int32_t *seq_start,
                    int32_t head_dim, int64_t v_row_stride, int64_t vt_ld,
                    void *stream);
 
+
+/* Zero the V^T columns [vt_start[s] + seq_len[s], vt_start[s] + seq_len[s]
+ * rounded up to 64) of rows [0, vt_rows), for every sequence s: the tail
+ * dx_attn_prefill_vt reads as zero keys' values. dx_transpose_v writes these
+ * itself; a caller that fills V^T through dx_qkv_rope calls this once per
+ * batch layout (the projection writes only columns below seq_len). Layout
+ * helper, no reference counterpart. */
+int dx_vt_zero_tails(void *vt, const int32_t *seq_len, const int32_t *vt_start,
+                     int32_t num_seqs, int32_t vt_rows, int64_t vt_ld,
+                     void *stream);
+
 /* ------------------------------------------------------------------------ */
 /* Projections and MLP                                                       */
 /* ------------------------------------------------------------------------ */
@@ -137,6 +148,29 @@ int dx_linear(const void *x, const void *w, void *y, int64_t m, int64_t n,
 int dx_gated_linear(const void *x, const void *gate_up, void *act, int64_t m,
                     int64_t f, int64_t k, int64_t ldx, int64_t ld_act,
                     int32_t activation, void *stream);
+
+/* Fused QKV projection. With w_qkv the packed [(Hq + 2 Hkv) D, hidden]
+ * weight (rows q | k | v), t = bf16(x @ w_qkv^T) (fp32 accumulation), and:
+ *   q | k heads (columns [0, (Hq + Hkv) D)): rotate-half RoPE at
+ *     positions[row] with the formula and rounding of dx_rope, into
+ *     qk[row * ld_qk + col];
+ *   v (columns (Hq + Hkv) D + g D + d): into
+ *     vt[(g D + d) * vt_ld + vt_col[row]], the V^T layout of
+ *     dx_attn_prefill_vt (vt_col[row] = vt_start[s] + p for row
+ *     seq_start[s] + p). Columns past each seq_len are not written
+ *     (dx_vt_zero_tails).
+ * Replaces the packed projection with RoPE in the epilogue of
+ * src/deciax/kernels/fused.py:93-99,120-122 (and the per-layer `apply_rope`
+ * of src/deciax/nn.py:35-44 on the q / k split of
+ * src/deciax/models/qwen3_5/text.py:75-91). Requires (Hq + 2 Hkv) D % 256
+ * == 0, hidden % 64 == 0, head_dim in {64, 128, 256}; cos/sin are bf16
+ * [max_pos, D / 2]. */
+int dx_qkv_rope(const void *x, const void *w_qkv, void *qk, void *vt,
+                const int32_t *positions, const int32_t *vt_col,
+                const void *cos, const void *sin, int64_t rows,
+                int64_t hidden, int32_t num_q_heads, int32_t num_kv_heads,
+                int32_t head_dim, int64_t ldx, int64_t ld_qk, int64_t vt_ld,
+                int32_t max_pos, void *stream);
 
 /* Pack gate[f, k] and up[f, k] (PyTorch layout) into the [2f, k] layout of
  * dx_gated_linear: rows [128 b, 128 b + 64) are gate rows [64 b, 64 b + 64)

@@ -398,6 +398,49 @@ def test_rope(d: int) -> None:
     np.testing.assert_array_equal(got[:, heads * d:], x[:, heads * d:])
 
 
+@pytest.mark.parametrize("lengths,hq,hkv,d,hidden", [
+    ([37, 200, 129, 64], 4, 2, 256, 512),   # BM 128 row tiles
+    ([700, 555], 4, 2, 128, 384),           # BM 256 row tiles
+    ([90, 31, 300], 2, 1, 128, 256),        # q|k and v share a column tile
+    ([65, 64, 1], 4, 2, 64, 192),
+])
+def test_qkv_rope_matches_unfused(lengths: list[int], hq: int, hkv: int, d: int, hidden: int) -> None:
+    """The fused projection (RoPE in the epilogue, V written transposed) is bit-identical to
+    linear -> rope -> transpose_v, which the tests above pin against the oracle."""
+    import torch
+
+    from deciax_amd import gemma
+    from deciax_amd import kernels as K
+
+    say(f"qkv_rope lengths={lengths} hq={hq} hkv={hkv} d={d} hidden={hidden}")
+    r = rng(len(lengths) + d)
+    batch = gemma.pack_batch([r.integers(0, 100, n).tolist() for n in lengths], [[] for _ in lengths])
+    rows, width = batch.rows, (hq + 2 * hkv) * d
+    qd, kd = hq * d, hkv * d
+    x = to_dev(bf16_np(r.normal(size=(rows, hidden))))
+    w = to_dev(bf16_np(r.normal(size=(width, hidden)) * 0.05))
+    cos_b, sin_b = gemma.rope_tables(4096, d, 10000.0)
+    cos, sin = gemma._bits_to_tensor(cos_b, x.device), gemma._bits_to_tensor(sin_b, x.device)
+
+    ref = K.linear(x, w)
+    K.rope(ref, batch.positions, cos, sin, num_heads=hq + hkv, head_dim=d)
+    vt_ref = torch.zeros((kd, batch.vt_ld), dtype=torch.bfloat16, device=x.device)
+    K.transpose_v(ref[:, qd + kd:], vt_ref, batch.seq_start, batch.seq_len, batch.vt_start, batch.max_len,
+                  num_kv_heads=hkv, head_dim=d)
+
+    qk = torch.full((rows, width), float("nan"), dtype=torch.bfloat16, device=x.device)
+    vt = torch.full((kd, batch.vt_ld + 8), float("nan"), dtype=torch.bfloat16, device=x.device)[:, :batch.vt_ld]
+    K.vt_zero_tails(vt, batch.seq_len, batch.vt_start)
+    K.qkv_rope(x, w, qk, vt, batch.positions, batch.vt_col, cos, sin, num_q_heads=hq, num_kv_heads=hkv, head_dim=d)
+    torch.cuda.synchronize()
+    def bits(t: torch.Tensor) -> np.ndarray:
+        return t.contiguous().view(torch.int16).cpu().numpy()
+
+    np.testing.assert_array_equal(bits(qk[:, :qd + kd]), bits(ref[:, :qd + kd]))
+    assert torch.isnan(qk[:, qd + kd:].float()).all(), "the V columns of qk are not written"
+    np.testing.assert_array_equal(bits(vt), bits(vt_ref))
+
+
 def test_readout() -> None:
     from deciax_amd import kernels as K
     from oracle.model import readout
