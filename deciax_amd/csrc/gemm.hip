@@ -215,7 +215,26 @@ gemm_nt_kernel(const uint16_t *__restrict__ A, const uint16_t *__restrict__ B, v
           if (row < M) Cf[(long)row * ldc + col] = acc[i][j][r];
         }
   } else {
-    // Stage the bf16 tile through LDS, then store 16-byte row chunks.
+    // Stage the bf16 tile through LDS, then store 16-byte row chunks. A QKV tile made only of v
+    // columns is staged transposed ([col][row], pitch BM + 8): its stores walk V^T rows.
+    const bool vt_tile = EPI == EPI_QKV && n0 >= qe.qk_cols;
+    if (vt_tile) {
+      constexpr int TP = BM + 8;
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; r += 4) {
+          const int row = wm * (BM / 2) + i * 32 + (r >> 2) * 8 + lhalf * 4;
+#pragma unroll
+          for (int j = 0; j < TN; ++j) {
+            const int col = wn * (BN / 2) + j * 32 + lrow;
+            u32x2 w;
+            w[0] = pack_bf2(acc[i][j][r], acc[i][j][r + 1]);
+            w[1] = pack_bf2(acc[i][j][r + 2], acc[i][j][r + 3]);
+            *reinterpret_cast<u32x2 *>(smem + col * TP + row) = w;
+          }
+        }
+    } else
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
@@ -244,7 +263,7 @@ gemm_nt_kernel(const uint16_t *__restrict__ A, const uint16_t *__restrict__ B, v
     if constexpr (EPI == EPI_QKV) {
       // q / k heads (head columns below qk_cols): item = (row, head, 8 rotary pairs j0..j0+7)
       const int d = qe.d, half = d / 2, per_head = d / 16;
-      for (int idx = tid; idx < BM * (BN / 16); idx += THREADS) {
+      for (int idx = vt_tile ? BM * (BN / 16) : tid; idx < BM * (BN / 16); idx += THREADS) {
         const int row = idx / (BN / 16), rem = idx % (BN / 16);
         const int j0 = (rem % per_head) * 8, c1 = (rem / per_head) * d + j0;
         if (m0 + row >= M || n0 + c1 >= qe.qk_cols) continue;
@@ -271,9 +290,29 @@ gemm_nt_kernel(const uint16_t *__restrict__ A, const uint16_t *__restrict__ B, v
         *reinterpret_cast<u32x4 *>(dst) = o1;
         *reinterpret_cast<u32x4 *>(dst + half) = o2;
       }
-      // v (columns from qk_cols on): tile column c is V^T row n0 + c - qk_cols. A thread keeps one
-      // row (token), so the lanes of a store instruction write consecutive V^T columns.
-      if (n0 + BN > qe.qk_cols) {
+      if (vt_tile) {
+        // Thread c owns V^T row n0 + c - qk_cols and walks the tile's tokens: 8 tokens whose V^T columns
+        // are consecutive and 8-aligned go out as one 16-byte store, others one by one. The walk
+        // depends on the rows only, so every thread takes the same branches.
+        constexpr int TP = BM + 8;
+        const int valid = min(BM, M - m0);
+        for (int c = tid; c < BN; c += THREADS) {
+          uint16_t *vrow = qe.vt + (long)(n0 + c - qe.qk_cols) * qe.vt_ld;
+          const uint16_t *src = smem + c * TP;
+          for (int r = 0; r < valid;) {
+            const int col = qe.vt_col[m0 + r];
+            if ((col & 7) == 0 && r + 8 <= valid && qe.vt_col[m0 + r + 7] == col + 7) {
+              *reinterpret_cast<u32x4 *>(vrow + col) = *reinterpret_cast<const u32x4 *>(src + r);
+              r += 8;
+            } else {
+              vrow[col] = src[r];
+              r += 1;
+            }
+          }
+        }
+      } else if (n0 + BN > qe.qk_cols) {
+        // a tile holding both q|k and v columns: v one element at a time (tile column c is V^T row
+        // n0 + c - qk_cols; the lanes of a store instruction write consecutive V^T columns)
         const int row = tid % BM;
         if (m0 + row < M) {
           const long col = qe.vt_col[m0 + row];

@@ -2,14 +2,18 @@
 
 `load(model, *, revision, dtype, impl)` builds a Gemma-2-shaped decision model
 on the MI355X and binds it to an engine; `Decider.decide` / `decide_batch`
-keep the reference's signatures. The models here are synthetic (random-init
-weights of the named shape, seeded) because no checkpoint is available; the
-path they exercise is the one a real checkpoint would take.
+keep the reference's signatures. `model` is either a registered shape (random-init
+weights, seeded) or a local Gemma-2 checkpoint directory (config.json plus
+safetensors, read by `deciax_amd.checkpoint`). The reference resolves a Hub name
+with `snapshot_download` (src/deciax/decider.py:66-73); there is no network here,
+so a checkpoint must already be on disk.
 """
 
 from __future__ import annotations
 
 from collections.abc import Mapping, Sequence
+from dataclasses import replace
+from pathlib import Path
 from typing import Any, Literal
 
 from deciax_amd import gemma
@@ -39,30 +43,35 @@ class Decider:
         return self.engine.decide_batch(states, questions, max_len=max_len, head_max_len=head_max_len)
 
 
-def load(model: ModelName = "gemma2-9b", *, revision: str | None = None, dtype: DtypeChoice = "auto",
+def load(model: ModelName | str | Path = "gemma2-9b", *, revision: str | None = None, dtype: DtypeChoice = "auto",
          impl: ImplChoice = "auto", seed: int = 0, tokenizer: TokenizerLike | None = None,
          layers: int | None = None) -> Decider:
-    """Build a synthetic decision model of a registered shape on the GPU.
+    """Build a decision model on the GPU: a registered shape with seeded random weights, or a
+    Gemma-2 checkpoint directory.
 
     `impl` resolves as in `deciax_amd.backend.resolve`; the HIP path computes in bf16, so
     `dtype` must be "auto" or "bf16" (the reference likewise rejects Pallas without BF16,
     src/deciax/models/clef/model.py:48-50). `layers` truncates the depth (tests only)."""
-    if model not in gemma.CONFIGS:
-        raise ValueError(f"unknown model {model!r}; choose one of {sorted(gemma.CONFIGS)}")
+    is_dir = isinstance(model, (str, Path)) and Path(model).is_dir()
+    if not is_dir and model not in gemma.CONFIGS:
+        raise ValueError(f"unknown model {model!r}; choose one of {sorted(gemma.CONFIGS)} or a checkpoint directory")
     if revision is not None:
-        raise ValueError("synthetic models have no revisions")
+        raise ValueError("revisions need the Hub; pass a local checkpoint directory instead")
     if dtype not in ("auto", "bf16", "fp32"):
         raise ValueError(f"dtype must be 'auto', 'bf16' or 'fp32', got {dtype!r}")
     if dtype == "fp32":
         raise ValueError("the HIP decision forward requires bf16 weights")
     resolve(impl)
-    config = gemma.CONFIGS[model]
+    if is_dir:
+        from deciax_amd import checkpoint
+
+        config, host = checkpoint.read_checkpoint(model)
+    else:
+        config, host = gemma.CONFIGS[model], None
     if layers is not None:
         if not 1 <= layers <= config.layers:
             raise ValueError(f"layers must be in [1, {config.layers}]")
-        from dataclasses import replace
-
         config = replace(config, layers=layers)
-    weights = gemma.random_weights(config, seed=seed)
+    weights = gemma.weights_from_host(config, host) if host is not None else gemma.random_weights(config, seed=seed)
     tok = tokenizer if tokenizer is not None else ByteTokenizer(config.vocab)
-    return Decider(DecisionEngine(weights, tok, model))
+    return Decider(DecisionEngine(weights, tok, config.name if is_dir else model))

@@ -132,6 +132,59 @@ def test_27b_shape_two_layers_matches_oracle() -> None:
     _check(probs.cpu().numpy(), w.numpy_weights(), cfg, batch)
 
 
+def test_checkpoint_directory_forward_matches_oracle(tmp_path) -> None:
+    """A Gemma-2 checkpoint on disk (Hugging Face names, sharded safetensors plus index, config.json)
+    through deciax_amd.checkpoint: the forward on the loaded weights meets the oracle on the same
+    weights, and deciax_amd.load accepts the directory."""
+    import json
+
+    import torch
+    from dataclasses import replace
+    from safetensors.torch import save_file
+
+    import deciax_amd
+    from deciax_amd import checkpoint, gemma
+
+    say("checkpoint directory -> forward")
+    cfg = replace(gemma.CONFIGS["tiny"], layers=2)
+    src = gemma.random_weights(cfg, seed=11, keep_unpacked=True, norm_std=0.3)
+    host = src.numpy_weights()
+    to_hf = {v: k for k, v in checkpoint.LAYER_NAMES.items()}
+    named = {"model.embed_tokens.weight": host["embed"], "model.norm.weight": host["final_norm"]}
+    for key, value in host.items():
+        if key.startswith("layers."):
+            _, i, name = key.split(".", 2)
+            named[f"model.layers.{i}.{to_hf[name]}"] = value
+    keys = sorted(named)
+    shards = {f"model-{j + 1:05d}-of-00002.safetensors": keys[j::2] for j in range(2)}
+    for fname, ks in shards.items():
+        save_file({k: torch.from_numpy(np.ascontiguousarray(named[k])).to(torch.bfloat16) for k in ks},
+                  str(tmp_path / fname))
+    (tmp_path / "model.safetensors.index.json").write_text(
+        json.dumps({"metadata": {}, "weight_map": {k: f for f, ks in shards.items() for k in ks}}))
+    (tmp_path / "config.json").write_text(json.dumps({
+        "model_type": "gemma2", "num_hidden_layers": cfg.layers, "hidden_size": cfg.hidden,
+        "num_attention_heads": cfg.heads, "num_key_value_heads": cfg.kv_heads, "head_dim": cfg.head_dim,
+        "intermediate_size": cfg.intermediate, "vocab_size": cfg.vocab, "sliding_window": cfg.window,
+        "attn_logit_softcapping": cfg.attn_softcap, "final_logit_softcapping": cfg.final_softcap,
+        "query_pre_attn_scalar": cfg.query_pre_attn_scalar, "rms_norm_eps": cfg.eps,
+        "rope_parameters": {"rope_theta": cfg.rope_theta, "rope_type": "default"},
+        "hidden_activation": "gelu_pytorch_tanh", "max_position_embeddings": cfg.max_position,
+        "layer_types": ["sliding_attention", "full_attention"], "tie_word_embeddings": True}))
+
+    w = checkpoint.load_weights(tmp_path, keep_unpacked=True)
+    assert w.config.query_scale == cfg.query_scale and w.config.window == cfg.window
+    ids, options = _batch([150, 41], cfg.vocab, 3, seed=13)
+    batch = gemma.pack_batch(ids, options)
+    logits, probs = gemma.forward(w, batch)
+    torch.cuda.synchronize()
+    _check(probs.cpu().numpy(), w.numpy_weights(), w.config, batch)
+    _, probs_src = gemma.forward(src, batch)
+    np.testing.assert_array_equal(probs.cpu().numpy(), probs_src.cpu().numpy())
+    d = deciax_amd.load(str(tmp_path), impl="hip")
+    assert d.decide("a loaded checkpoint", {"ok": {"type": "noul"}})["answers"]["ok"]["noul"] >= 0
+
+
 def test_decide_end_to_end() -> None:
     import deciax_amd
 
