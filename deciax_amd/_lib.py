@@ -22,7 +22,7 @@ HEADER = Path(__file__).resolve().parent.parent / "include" / "deciax_hip.h"
 
 DX_OK, DX_ERR_INVALID, DX_ERR_UNSUPPORTED, DX_ERR_RUNTIME = 0, 1, 2, 3
 DX_BF16, DX_F32 = 0, 1
-DX_ACT_GELU_TANH, DX_ACT_SILU = 0, 1
+DX_ACT_GELU_TANH, DX_ACT_SILU, DX_ACT_GELU_ERF, DX_ACT_NONE = 0, 1, 2, 3
 
 _p = c_void_p
 _i32p = POINTER(c_int32)
@@ -69,6 +69,23 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
         c_int,
         [_p, _p, _p, _p, _p, _p, c_int32, c_int64, c_int64, c_int64, c_int64, c_int64, c_float, c_float, _p, _p, _p],
     ),
+    "dx_layer_norm_f32": (c_int, [_p, _p, _p, _p, c_int64, c_int64, c_int64, c_int64, c_float, _p]),
+    "dx_linear_f32": (
+        c_int, [_p, _p, _p, _p, c_int64, c_int64, c_int64, c_int64, c_int64, c_int64, c_int32, c_int32, _p]),
+    "dx_span_means_f32": (c_int, [_p, _p, _p, c_int32, c_int32, c_int32, c_int64, c_int64, c_int64, _p]),
+    "dx_mha_f32": (
+        c_int,
+        [_p, _p, _p, _p, _p, c_int32, c_int32, c_int32, c_int32, c_int32, c_int64, c_int64, c_int64, c_int64, _p],
+    ),
+    "dx_gather_rows_f32": (
+        c_int, [_p, _p, _p, c_int32, c_int32, c_int32, c_int64, c_int64, c_int64, c_int32, _p]),
+    "dx_head_routing_f32": (c_int, [_p, _p, _p, _p, _p, c_int32, c_int32, c_int32, c_int32, _p]),
+    "dx_head_fields_init_f32": (c_int, [_p, _p, _p, _p, _p, _p, c_int32, c_int32, c_int32, c_int32, _p]),
+    "dx_head_features_f32": (
+        c_int,
+        [_p, _p, _p, _p, _p, _p, _p, _p, _p, c_int32, c_int32, c_int32, c_int32, c_int32, c_float, _p],
+    ),
+    "dx_head_combine_f32": (c_int, [_p, _p, _p, _p, _p, c_int64, c_float, c_float, _p]),
 }
 
 _LIB: ctypes.CDLL | None = None

@@ -19,7 +19,7 @@ ROOT = PKG.parent
 CSRC = PKG / "csrc"
 INCLUDE = ROOT / "include"
 LIB = PKG / "libdeciax_hip.so"
-SOURCES = ("abi.hip", "gemm.hip", "attention.hip", "rowwise.hip")
+SOURCES = ("abi.hip", "gemm.hip", "attention.hip", "rowwise.hip", "head.hip")
 ARCH = "gfx950"
 
 # Packed-fp32 VALU forms stay disabled in every device compile.

@@ -381,3 +381,114 @@ int dx_readout(const void *hidden, const void *norm_w, const void *table, const 
 }
 
 }  // extern "C"
+
+/* ------------------------------------------------------------------------ */
+/* Clef joint schema head (fp32)                                             */
+/* ------------------------------------------------------------------------ */
+
+int dx_layer_norm_f32(const float *x, const float *w, const float *b, float *y, int64_t rows, int64_t d, int64_t ldx,
+                      int64_t ldy, float eps, void *stream) {
+  REQUIRE(x && w && y, "layer_norm: null pointer argument");
+  REQUIRE(rows >= 0 && d > 0 && ldx >= d && ldy >= d && eps >= 0.f, "layer_norm: bad sizes");
+  if (rows == 0) return DX_OK;
+  return check_launch(dx_layer_norm_f32_launch(x, w, b, y, rows, (int)d, ldx, ldy, eps, as_stream(stream)),
+                      "layer_norm launch");
+}
+
+int dx_linear_f32(const float *x, const float *w, const float *bias, float *y, int64_t m, int64_t n, int64_t k,
+                  int64_t ldx, int64_t ldw, int64_t ldy, int32_t activation, int32_t accumulate, void *stream) {
+  REQUIRE(x && w && y, "linear_f32: null pointer argument");
+  REQUIRE(m >= 0 && n > 0 && k > 0 && ldx >= k && ldw >= k && ldy >= n, "linear_f32: bad sizes");
+  REQUIRE(activation == DX_ACT_NONE || activation == DX_ACT_GELU_ERF,
+          "linear_f32: activation %d not in {DX_ACT_NONE, DX_ACT_GELU_ERF}", activation);
+  SUPPORTED(n < (1L << 30) && k < (1L << 30), "linear_f32: n, k must fit 30 bits");
+  if (m == 0) return DX_OK;
+  return check_launch(dx_linear_f32_launch(x, w, bias, y, m, (int)n, (int)k, ldx, ldw, ldy,
+                                           activation == DX_ACT_GELU_ERF ? 1 : 0,
+                                           accumulate ? 1 : 0, as_stream(stream)),
+                      "linear_f32 launch");
+}
+
+int dx_span_means_f32(const float *x, const int32_t *spans, float *out, int32_t batch, int32_t seq, int32_t spans_per_row,
+                      int64_t d, int64_t ldx, int64_t ld_out, void *stream) {
+  REQUIRE(x && spans && out, "span_means: null pointer argument");
+  REQUIRE(batch >= 0 && seq > 0 && spans_per_row >= 0 && d > 0 && ldx >= d && ld_out >= d, "span_means: bad sizes");
+  if (batch == 0 || spans_per_row == 0) return DX_OK;
+  return check_launch(dx_span_means_f32_launch(x, spans, out, batch, seq, spans_per_row, (int)d, ldx, ld_out,
+                                               as_stream(stream)),
+                      "span_means launch");
+}
+
+int dx_mha_f32(const float *q, const float *k, const float *v, const uint8_t *key_mask, float *out, int32_t batch,
+               int32_t num_queries, int32_t num_keys, int32_t heads, int32_t head_dim, int64_t ldq, int64_t ldk,
+               int64_t ldv, int64_t ld_out, void *stream) {
+  REQUIRE(q && k && v && key_mask && out, "mha_f32: null pointer argument");
+  REQUIRE(batch >= 0 && num_queries >= 0 && num_keys > 0 && heads > 0 && head_dim > 0, "mha_f32: bad sizes");
+  const int64_t width = (int64_t)heads * head_dim;
+  REQUIRE(ldq >= width && ldk >= width && ldv >= width && ld_out >= width, "mha_f32: row strides below heads * head_dim");
+  SUPPORTED(num_keys <= 32768, "mha_f32: %d keys above 32768", num_keys);
+  if (batch == 0 || num_queries == 0) return DX_OK;
+  return check_launch(dx_mha_f32_launch(q, k, v, key_mask, out, batch, num_queries, num_keys, heads, head_dim, ldq, ldk,
+                                        ldv, ld_out, as_stream(stream)),
+                      "mha_f32 launch");
+}
+
+int dx_gather_rows_f32(const float *x, const int32_t *index, float *y, int32_t batch, int32_t rows_per_batch,
+                       int32_t picks_per_batch, int64_t d, int64_t ldx, int64_t ldy, int32_t accumulate, void *stream) {
+  REQUIRE(x && index && y, "gather_rows: null pointer argument");
+  REQUIRE(batch >= 0 && rows_per_batch > 0 && picks_per_batch >= 0 && d > 0 && ldx >= d && ldy >= d,
+          "gather_rows: bad sizes");
+  if (batch == 0 || picks_per_batch == 0) return DX_OK;
+  return check_launch(dx_gather_rows_f32_launch(x, index, y, batch, rows_per_batch, picks_per_batch, (int)d, ldx, ldy,
+                                                accumulate ? 1 : 0, as_stream(stream)),
+                      "gather_rows launch");
+}
+
+int dx_head_routing_f32(const float *options, const float *base, const int32_t *option_field,
+                        const uint8_t *option_mask, float *summary, int32_t batch, int32_t num_options,
+                        int32_t num_fields, int32_t width, void *stream) {
+  REQUIRE(options && base && option_field && option_mask && summary, "head_routing: null pointer argument");
+  REQUIRE(batch >= 0 && num_options > 0 && num_fields >= 0 && width > 0, "head_routing: bad sizes");
+  SUPPORTED(num_options <= 16384, "head_routing: %d options above 16384", num_options);
+  if (batch == 0 || num_fields == 0) return DX_OK;
+  return check_launch(dx_routing_f32_launch(options, base, option_field, option_mask, summary, batch, num_options,
+                                            num_fields, width, as_stream(stream)),
+                      "head_routing launch");
+}
+
+int dx_head_fields_init_f32(const float *base, const float *summary_norm, const float *global_proj,
+                            const float *type_embedding, const int32_t *types, float *fields, int32_t batch,
+                            int32_t num_fields, int32_t width, int32_t num_types, void *stream) {
+  REQUIRE(base && summary_norm && global_proj && type_embedding && types && fields,
+          "head_fields_init: null pointer argument");
+  REQUIRE(batch >= 0 && num_fields >= 0 && width > 0 && num_types > 0, "head_fields_init: bad sizes");
+  if (batch == 0 || num_fields == 0) return DX_OK;
+  return check_launch(dx_fields_init_f32_launch(base, summary_norm, global_proj, type_embedding, types, fields, batch,
+                                                num_fields, width, num_types, as_stream(stream)),
+                      "head_fields_init launch");
+}
+
+int dx_head_features_f32(const float *fields, const float *options, const float *questions, const float *global_vector,
+                         const float *lexical, const int32_t *option_field, float *features, float *prior,
+                         float *cosine, int32_t batch, int32_t num_options, int32_t num_fields, int32_t width,
+                         int32_t hidden, float prior_scale, void *stream) {
+  REQUIRE(fields && options && questions && global_vector && lexical && option_field && features && prior && cosine,
+          "head_features: null pointer argument");
+  REQUIRE(batch >= 0 && num_options >= 0 && num_fields > 0 && width > 0 && hidden > 0, "head_features: bad sizes");
+  if (batch == 0 || num_options == 0) return DX_OK;
+  return check_launch(dx_features_f32_launch(fields, options, questions, global_vector, lexical, option_field, features,
+                                             prior, cosine, batch, num_options, num_fields, width, hidden, prior_scale,
+                                             as_stream(stream)),
+                      "head_features launch");
+}
+
+int dx_head_combine_f32(const float *prior, const float *cosine, const float *residual, const uint8_t *option_mask,
+                        float *logits, int64_t n, float gate, float joint_scale, void *stream) {
+  REQUIRE(prior && cosine && residual && option_mask && logits, "head_combine: null pointer argument");
+  REQUIRE(n >= 0, "head_combine: bad size");
+  if (n == 0) return DX_OK;
+  return check_launch(dx_combine_f32_launch(prior, cosine, residual, option_mask, logits, n, gate, joint_scale,
+                                            as_stream(stream)),
+                      "head_combine launch");
+}
+

@@ -64,3 +64,28 @@ hipError_t dx_readout_launch(const uint16_t *hidden, const uint16_t *norm_w, con
                              hipStream_t s);
 hipError_t dx_pack_gate_up_launch(const uint16_t *gate, const uint16_t *up, uint16_t *packed, long f, long k,
                                   hipStream_t s);
+
+// Clef joint-head operations (head.hip), fp32.
+hipError_t dx_layer_norm_f32_launch(const float *x, const float *w, const float *b, float *y, long rows, int d,
+                                    long ldx, long ldy, float eps, hipStream_t s);
+hipError_t dx_linear_f32_launch(const float *x, const float *w, const float *bias, float *y, long m, int n, int k,
+                                long ldx, long ldw, long ldy, int act, int acc, hipStream_t s);
+hipError_t dx_span_means_f32_launch(const float *x, const int32_t *spans, float *out, int B, int S, int O, int d,
+                                    long ldx, long ldo, hipStream_t s);
+hipError_t dx_mha_f32_launch(const float *q, const float *k, const float *v, const uint8_t *key_mask, float *out,
+                             int B, int Q, int K, int H, int dh, long ldq, long ldk, long ldv, long ldo, hipStream_t s);
+hipError_t dx_gather_rows_f32_launch(const float *x, const int32_t *idx, float *y, int B, int R, int I, int d,
+                                     long ldx, long ldy, int acc, hipStream_t s);
+hipError_t dx_routing_f32_launch(const float *options, const float *base, const int32_t *owner,
+                                 const uint8_t *option_mask, float *summary, int B, int O, int NQ, int W,
+                                 hipStream_t s);
+hipError_t dx_fields_init_f32_launch(const float *base, const float *sn, const float *glob, const float *type_emb,
+                                     const int32_t *types, float *fields, int B, int NQ, int W, int num_types,
+                                     hipStream_t s);
+hipError_t dx_features_f32_launch(const float *fields, const float *opts, const float *questions, const float *glob,
+                                  const float *lexical, const int32_t *owner, float *features, float *prior,
+                                  float *cosine, int B, int O, int NQ, int W, int Hd, float prior_scale,
+                                  hipStream_t s);
+hipError_t dx_combine_f32_launch(const float *prior, const float *cosine, const float *residual,
+                                 const uint8_t *option_mask, float *out, long n, float gate, float joint_scale,
+                                 hipStream_t s);

@@ -15,7 +15,7 @@ from collections.abc import Sequence
 import torch
 
 from deciax_amd import _lib
-from deciax_amd._lib import DX_ACT_GELU_TANH, DX_ACT_SILU, DX_BF16, DX_F32, call
+from deciax_amd._lib import DX_ACT_GELU_ERF, DX_ACT_GELU_TANH, DX_ACT_NONE, DX_ACT_SILU, DX_BF16, DX_F32, call
 
 BF16 = torch.bfloat16
 F32 = torch.float32
@@ -377,6 +377,120 @@ def readout(hidden: torch.Tensor, norm_w: torch.Tensor, table: torch.Tensor, opt
          float(softcap),
          _ptr(logits), _ptr(probs), _stream())
     return logits, probs
+
+
+# ---------------------------------------------------------------------------- Clef joint head (fp32)
+
+
+def _f32(t: torch.Tensor, name: str, ndim: int = 2) -> None:
+    _need(t, name, F32, ndim)
+
+
+def layer_norm_f32(x: torch.Tensor, w: torch.Tensor, b: torch.Tensor | None, *, eps: float,
+                   out: torch.Tensor | None = None) -> torch.Tensor:
+    """Row LayerNorm in fp32 (`layer_norm`, src/deciax/nn.py:22-29)."""
+    _f32(x, "x")
+    out = torch.empty_like(x) if out is None else out
+    _f32(out, "out")
+    call("dx_layer_norm_f32", _ptr(x), _ptr(w), _ptr(b), _ptr(out), x.shape[0], x.shape[1], _rows(x, "x"),
+         _rows(out, "out"), float(eps), _stream())
+    return out
+
+
+def linear_f32(x: torch.Tensor, w: torch.Tensor, bias: torch.Tensor | None = None, *, gelu: bool = False,
+               out: torch.Tensor | None = None, accumulate: bool = False) -> torch.Tensor:
+    """out (+)= act(x @ w^T + bias) in fp32; act = exact GELU when `gelu` (`dense`,
+    src/deciax/models/qwen3_5/text.py:21-22, with the head's residual adds)."""
+    _f32(x, "x")
+    _f32(w, "w")
+    if out is None:
+        if accumulate:
+            raise ValueError("linear_f32: accumulate needs out")
+        out = torch.empty((x.shape[0], w.shape[0]), dtype=F32, device=x.device)
+    _f32(out, "out")
+    if x.shape[1] != w.shape[1] or out.shape != (x.shape[0], w.shape[0]):
+        raise ValueError(f"linear_f32: shapes {tuple(x.shape)} x {tuple(w.shape)}^T -> {tuple(out.shape)}")
+    call("dx_linear_f32", _ptr(x), _ptr(w), _ptr(bias), _ptr(out), x.shape[0], w.shape[0], x.shape[1], _rows(x, "x"),
+         _rows(w, "w"), _rows(out, "out"), DX_ACT_GELU_ERF if gelu else DX_ACT_NONE, int(accumulate), _stream())
+    return out
+
+
+def span_means_f32(x: torch.Tensor, spans: torch.Tensor, *, batch: int) -> torch.Tensor:
+    """x [batch * S, d] rows, spans [batch, n, 2] -> [batch * n, d] (`means`, head.py:24-29)."""
+    _f32(x, "x")
+    _need(spans, "spans", torch.int32, 3)
+    n = spans.shape[1]
+    out = torch.empty((batch * n, x.shape[1]), dtype=F32, device=x.device)
+    call("dx_span_means_f32", _ptr(x), _ptr(spans), _ptr(out), batch, x.shape[0] // batch, n, x.shape[1],
+         _rows(x, "x"), _rows(out, "out"), _stream())
+    return out
+
+
+def mha_f32(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, key_mask: torch.Tensor, *, batch: int,
+            heads: int) -> torch.Tensor:
+    """Masked multi-head attention core over [batch * n, heads * dh] rows (head.py:41-51)."""
+    for t, n in ((q, "q"), (k, "k"), (v, "v")):
+        _f32(t, n)
+    _need(key_mask, "key_mask", torch.uint8, 2)
+    width = q.shape[1]
+    nq, nk = q.shape[0] // batch, k.shape[0] // batch
+    if key_mask.shape != (batch, nk):
+        raise ValueError("mha_f32: key_mask must be [batch, num_keys]")
+    out = torch.empty((q.shape[0], width), dtype=F32, device=q.device)
+    call("dx_mha_f32", _ptr(q), _ptr(k), _ptr(v), _ptr(key_mask), _ptr(out), batch, nq, nk, heads, width // heads,
+         _rows(q, "q"), _rows(k, "k"), _rows(v, "v"), _rows(out, "out"), _stream())
+    return out
+
+
+def gather_rows_f32(x: torch.Tensor, index: torch.Tensor, *, batch: int, out: torch.Tensor | None = None,
+                    accumulate: bool = False) -> torch.Tensor:
+    """out[b * I + i] (+)= x[b * R + index[b, i]] (`gather`, head.py:32-33)."""
+    _f32(x, "x")
+    _need(index, "index", torch.int32, 2)
+    picks = index.shape[1]
+    if out is None:
+        out = torch.empty((batch * picks, x.shape[1]), dtype=F32, device=x.device)
+    call("dx_gather_rows_f32", _ptr(x), _ptr(index), _ptr(out), batch, x.shape[0] // batch, picks, x.shape[1],
+         _rows(x, "x"), _rows(out, "out"), int(accumulate), _stream())
+    return out
+
+
+def head_routing_f32(options: torch.Tensor, base: torch.Tensor, option_field: torch.Tensor,
+                     option_mask: torch.Tensor, *, batch: int) -> torch.Tensor:
+    """Per-field softmax over the owned options and the routed summary (head.py:77-85)."""
+    out = torch.empty_like(base)
+    call("dx_head_routing_f32", _ptr(options), _ptr(base), _ptr(option_field), _ptr(option_mask), _ptr(out), batch,
+         options.shape[0] // batch, base.shape[0] // batch, base.shape[1], _stream())
+    return out
+
+
+def head_fields_init_f32(base: torch.Tensor, summary_norm: torch.Tensor, global_proj: torch.Tensor,
+                         type_embedding: torch.Tensor, types: torch.Tensor, *, batch: int) -> torch.Tensor:
+    out = torch.empty_like(base)
+    call("dx_head_fields_init_f32", _ptr(base), _ptr(summary_norm), _ptr(global_proj), _ptr(type_embedding),
+         _ptr(types), _ptr(out), batch, base.shape[0] // batch, base.shape[1], type_embedding.shape[0], _stream())
+    return out
+
+
+def head_features_f32(fields: torch.Tensor, options: torch.Tensor, questions: torch.Tensor,
+                      global_vector: torch.Tensor, lexical: torch.Tensor, option_field: torch.Tensor, *, batch: int,
+                      prior_scale: float) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    n, width = fields.shape
+    features = torch.empty((n, 4 * width), dtype=F32, device=fields.device)
+    prior = torch.empty(n, dtype=F32, device=fields.device)
+    cosine = torch.empty(n, dtype=F32, device=fields.device)
+    call("dx_head_features_f32", _ptr(fields), _ptr(options), _ptr(questions), _ptr(global_vector), _ptr(lexical),
+         _ptr(option_field), _ptr(features), _ptr(prior), _ptr(cosine), batch, n // batch,
+         questions.shape[0] // batch, width, questions.shape[1], float(prior_scale), _stream())
+    return features, prior, cosine
+
+
+def head_combine_f32(prior: torch.Tensor, cosine: torch.Tensor, residual: torch.Tensor, option_mask: torch.Tensor, *,
+                     gate: float, joint_scale: float) -> torch.Tensor:
+    out = torch.empty_like(prior)
+    call("dx_head_combine_f32", _ptr(prior), _ptr(cosine), _ptr(residual), _ptr(option_mask), _ptr(out),
+         prior.numel(), float(gate), float(joint_scale), _stream())
+    return out
 
 
 def int32_device(values: Sequence[int] | torch.Tensor, device: torch.device | str) -> torch.Tensor:

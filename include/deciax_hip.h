@@ -37,7 +37,7 @@ enum dx_status {
 
 enum dx_dtype { DX_BF16 = 0, DX_F32 = 1 };
 
-enum dx_activation { DX_ACT_GELU_TANH = 0, DX_ACT_SILU = 1 };
+enum dx_activation { DX_ACT_GELU_TANH = 0, DX_ACT_SILU = 1, DX_ACT_GELU_ERF = 2, DX_ACT_NONE = 3 };
 
 /* Library identification and the calling thread's last error message. */
 const char *dx_version(void);
@@ -262,6 +262,95 @@ int dx_readout(const void *hidden, const void *norm_w, const void *table,
                int64_t num_options, int64_t hidden_rows, int64_t d,
                int64_t ld_hidden, int64_t vocab, float eps, float softcap,
                float *logits, float *probs, void *stream);
+
+/* ------------------------------------------------------------------------ */
+/* Clef joint schema head (fp32), the steps of                               */
+/* src/deciax/models/clef/head.py:54-111; deciax_amd/clef_head.py chains    */
+/* them in that order. Batched tensors are rows: row b * n + i of a         */
+/* [batch, n, d] tensor, each row ld* floats apart.                          */
+/* ------------------------------------------------------------------------ */
+
+/* y = (x - mean) * rsqrt(mean((x - mean)^2) + eps) * w + b per row, fp32
+ * (b nullable). Replaces `layer_norm` in src/deciax/nn.py:22-29 as the head's
+ * `norm` uses it (eps 1e-5, head.py:20-21). */
+int dx_layer_norm_f32(const float *x, const float *w, const float *b, float *y,
+                      int64_t rows, int64_t d, int64_t ldx, int64_t ldy,
+                      float eps, void *stream);
+
+/* y[m, n] = (accumulate ? y[m, n] : 0) + act(x @ w[n, k]^T + bias), fp32,
+ * act DX_ACT_NONE or DX_ACT_GELU_ERF (exact GELU, jax.nn.gelu with
+ * approximate=False). Replaces `linear` (src/deciax/nn.py:11-19) / `dense`
+ * (src/deciax/models/qwen3_5/text.py:21-22) with the head's residual adds
+ * (head.py:71-74,92-95) folded in. bias nullable. */
+int dx_linear_f32(const float *x, const float *w, const float *bias, float *y,
+                  int64_t m, int64_t n, int64_t k, int64_t ldx, int64_t ldw,
+                  int64_t ldy, int32_t activation, int32_t accumulate,
+                  void *stream);
+
+/* out[b, o] = mean of x[b, s] over s in [spans[b, o, 0], spans[b, o, 1])
+ * clipped to [0, seq); 0 for an empty span. Replaces `means`,
+ * src/deciax/models/clef/head.py:24-29. */
+int dx_span_means_f32(const float *x, const int32_t *spans, float *out,
+                      int32_t batch, int32_t seq, int32_t spans_per_row,
+                      int64_t d, int64_t ldx, int64_t ld_out, void *stream);
+
+/* Per batch row b, query i, head h: softmax over keys j (masked where
+ * key_mask[b, j] == 0, at MASK_FILL) of q_i . k_j / sqrt(head_dim), times v.
+ * The attention core of `mha`, src/deciax/models/clef/head.py:41-51, with the
+ * masking of src/deciax/kernels/attention/blocked.py:21-28 (non-causal). q,
+ * k, v, out hold heads * head_dim columns per row; num_keys <= 32768. */
+int dx_mha_f32(const float *q, const float *k, const float *v,
+               const uint8_t *key_mask, float *out, int32_t batch,
+               int32_t num_queries, int32_t num_keys, int32_t heads,
+               int32_t head_dim, int64_t ldq, int64_t ldk, int64_t ldv,
+               int64_t ld_out, void *stream);
+
+/* y[b, i] = (accumulate ? y[b, i] : 0) + x[b, index[b, i]] (index clamped to
+ * [0, rows_per_batch)). Replaces `gather`, src/deciax/models/clef/head.py:32-33. */
+int dx_gather_rows_f32(const float *x, const int32_t *index, float *y,
+                       int32_t batch, int32_t rows_per_batch,
+                       int32_t picks_per_batch, int64_t d, int64_t ldx,
+                       int64_t ldy, int32_t accumulate, void *stream);
+
+/* For field q of batch row b: routing = softmax over options o of
+ * options[b, o] . base[b, q] / sqrt(width), restricted to options with
+ * option_field[b, o] == q and option_mask[b, o]; summary[b, q] =
+ * sum_o routing[o] options[b, o]. Replaces head.py:77-85. Rows are dense
+ * ([batch, n, width] contiguous). */
+int dx_head_routing_f32(const float *options, const float *base,
+                        const int32_t *option_field, const uint8_t *option_mask,
+                        float *summary, int32_t batch, int32_t num_options,
+                        int32_t num_fields, int32_t width, void *stream);
+
+/* fields[b, q] = base[b, q] + summary_norm[b, q] + global_proj[b] +
+ * type_embedding[types[b, q]] (head.py:86-88). Dense rows. */
+int dx_head_fields_init_f32(const float *base, const float *summary_norm,
+                            const float *global_proj,
+                            const float *type_embedding, const int32_t *types,
+                            float *fields, int32_t batch, int32_t num_fields,
+                            int32_t width, int32_t num_types, void *stream);
+
+/* Per option (b, o) (head.py:98-106): prior = normalize(lexical[b, o]) .
+ * normalize(questions[b, f] + global_vector[b]) * prior_scale with
+ * f = option_field[b, o]; cosine = normalize(fields[b, o], 1e-8) .
+ * normalize(options[b, o], 1e-8); features[b, o] = [f, o, f * o, |f - o|]
+ * (4 width columns). fields / options have width columns, questions /
+ * global_vector / lexical hidden. Dense rows. */
+int dx_head_features_f32(const float *fields, const float *options,
+                         const float *questions, const float *global_vector,
+                         const float *lexical, const int32_t *option_field,
+                         float *features, float *prior, float *cosine,
+                         int32_t batch, int32_t num_options, int32_t num_fields,
+                         int32_t width, int32_t hidden, float prior_scale,
+                         void *stream);
+
+/* logits[i] = option_mask[i] ? prior[i] + gate * (joint_scale * cosine[i] +
+ * residual[i]) : -1e9 (head.py:107-111; gate = sigmoid(residual_gate),
+ * joint_scale = exp(min(joint_logit_scale, ln 100))). */
+int dx_head_combine_f32(const float *prior, const float *cosine,
+                        const float *residual, const uint8_t *option_mask,
+                        float *logits, int64_t n, float gate,
+                        float joint_scale, void *stream);
 
 #ifdef __cplusplus
 }
