@@ -1,0 +1,72 @@
+"""Argument validation of the C ABI, on the CPU.
+
+Every case here is rejected (or is an empty call) before the library touches the HIP runtime, so
+the calls are safe without a GPU. Each must return the documented status: DX_ERR_INVALID for
+malformed arguments, DX_ERR_UNSUPPORTED for shapes the kernels do not cover, and DX_OK for an
+empty problem. dx_last_error must then name the entry point."""
+
+from __future__ import annotations
+
+import ctypes
+
+import pytest
+
+from deciax_amd import _lib
+
+P = ctypes.c_void_p(0x10000)  # an aligned, non-null stand-in; never dereferenced by these calls
+NUL = None
+
+
+def lib():
+    return _lib.lib()
+
+
+def status(name: str, *args) -> int:
+    return getattr(lib(), name)(*args)
+
+
+def check(name: str, want: int, *args) -> None:
+    got = status(name, *args)
+    assert got == want, (name, got, want, lib().dx_last_error())
+    if want != _lib.DX_OK:
+        assert name.removeprefix("dx_").split("_f32")[0].split("_")[0] in lib().dx_last_error().decode()
+
+
+def qkv(rows=8, hidden=512, hq=4, hkv=2, d=128, ldx=512, ld_qk=768, vt_ld=64, max_pos=64, first=P):
+    return ("dx_qkv_rope", first, P, P, P, P, P, P, P, rows, hidden, hq, hkv, d, ldx, ld_qk, vt_ld, max_pos, NUL)
+
+
+def test_qkv_rope_validation() -> None:
+    check(*qkv()[:1], _lib.DX_ERR_INVALID, *qkv(first=NUL)[1:])
+    check(*qkv()[:1], _lib.DX_ERR_UNSUPPORTED, *qkv(d=96)[1:])                  # head_dim not in {64,128,256}
+    check(*qkv()[:1], _lib.DX_ERR_UNSUPPORTED, *qkv(hq=3, hkv=1, d=64)[1:])     # packed width 320
+    check(*qkv()[:1], _lib.DX_ERR_UNSUPPORTED, *qkv(hidden=500, ldx=504)[1:])   # hidden % 64
+    check(*qkv()[:1], _lib.DX_ERR_INVALID, *qkv(ld_qk=700)[1:])                 # below (hq + hkv) d
+    check(*qkv()[:1], _lib.DX_OK, *qkv(rows=0)[1:])
+
+
+def test_vt_zero_tails_validation() -> None:
+    check("dx_vt_zero_tails", _lib.DX_ERR_INVALID, P, P, P, 2, 16, 60, NUL)       # vt_ld % 8
+    check("dx_vt_zero_tails", _lib.DX_ERR_INVALID, NUL, P, P, 2, 16, 64, NUL)
+    check("dx_vt_zero_tails", _lib.DX_OK, P, P, P, 0, 16, 64, NUL)
+
+
+def test_head_op_validation() -> None:
+    check("dx_linear_f32", _lib.DX_ERR_INVALID, P, P, NUL, P, 4, 8, 8, 8, 8, 8, _lib.DX_ACT_SILU, 0, NUL)
+    check("dx_linear_f32", _lib.DX_ERR_INVALID, P, P, NUL, P, 4, 8, 8, 4, 8, 8, _lib.DX_ACT_NONE, 0, NUL)
+    check("dx_linear_f32", _lib.DX_OK, P, P, NUL, P, 0, 8, 8, 8, 8, 8, _lib.DX_ACT_GELU_ERF, 1, NUL)
+    check("dx_mha_f32", _lib.DX_ERR_UNSUPPORTED, P, P, P, P, P, 1, 4, 40000, 2, 8, 16, 16, 16, 16, NUL)
+    check("dx_mha_f32", _lib.DX_ERR_INVALID, P, P, P, P, P, 1, 4, 64, 2, 8, 15, 16, 16, 16, NUL)
+    check("dx_mha_f32", _lib.DX_OK, P, P, P, P, P, 1, 0, 64, 2, 8, 16, 16, 16, 16, NUL)
+    check("dx_layer_norm_f32", _lib.DX_ERR_INVALID, P, P, NUL, P, 4, 16, 8, 16, ctypes.c_float(1e-5), NUL)
+    check("dx_span_means_f32", _lib.DX_ERR_INVALID, P, P, P, 2, 0, 3, 16, 16, 16, NUL)
+    check("dx_gather_rows_f32", _lib.DX_ERR_INVALID, P, P, P, 2, 0, 3, 16, 16, 16, 0, NUL)
+    check("dx_head_routing_f32", _lib.DX_ERR_UNSUPPORTED, P, P, P, P, P, 1, 20000, 4, 16, NUL)
+    check("dx_head_combine_f32", _lib.DX_OK, P, P, P, P, P, 0, ctypes.c_float(0.5), ctypes.c_float(2.0), NUL)
+
+
+@pytest.mark.parametrize("name", sorted(_lib.SIGNATURES))
+def test_every_entry_point_has_a_signature_bound(name: str) -> None:
+    fn = getattr(lib(), name)
+    restype, argtypes = _lib.SIGNATURES[name]
+    assert fn.restype == restype and list(fn.argtypes) == list(argtypes)
