@@ -37,6 +37,11 @@
 
 namespace {
 
+template <int I>
+struct Int {
+  static constexpr int value = I;
+};
+
 constexpr int BK = 64;
 constexpr int BN = 256;
 constexpr int THREADS = 256;
@@ -164,10 +169,12 @@ gemm_nt_kernel(const uint16_t *__restrict__ A, const uint16_t *__restrict__ B, v
   gl(min(1, KT - 1), 0, NC);
   __syncthreads();
   rd(fa0, fb0, 0, 0);
-  for (int kt = 0; kt < KT; ++kt) {
-    // tile kt is in stage kt & 1; the registers hold tile kt + 1, which goes to the other stage
-    // while the registers refill with tile kt + 2 (clamped: the last tiles reload themselves).
-    const int st = kt & 1;
+  // One K tile; st (compile-time, hence the loop unrolled by two) is the stage holding tile kt. The
+  // registers hold tile kt + 1, which goes to the other stage while the registers refill with tile
+  // kt + 2 (clamped: the last tiles reload themselves). A constant stage keeps every LDS address a
+  // loop-invariant register plus an immediate.
+  auto iteration = [&](const int kt, auto stc) {
+    constexpr int st = decltype(stc)::value;
     const int k2 = min(kt + 2, KT - 1);
     __builtin_amdgcn_sched_barrier(0);
     sw(st ^ 1, 0, W0);
@@ -197,7 +204,13 @@ gemm_nt_kernel(const uint16_t *__restrict__ A, const uint16_t *__restrict__ B, v
     mm(fa1, fb1);
     DX_REGION(0, NG);
     __builtin_amdgcn_sched_barrier(0);
+  };
+  int kt = 0;
+  for (; kt + 1 < KT; kt += 2) {
+    iteration(kt, Int<0>());
+    iteration(kt + 1, Int<1>());
   }
+  if (kt < KT) iteration(kt, Int<0>());
 #undef DX_REGION
   asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
   __syncthreads();
