@@ -11,6 +11,10 @@ HBM before the timed region.
 Prints one JSON line: prefill tokens/s (value), decisions/s, TFLOP/s, the
 attention kernel's TFLOP/s and MFMA fraction, the dominant kernel's roofline,
 and the CPU oracle baseline timed on a bounded sample on this host.
+
+`--model gemma2-27b` runs the 27B shape instead (46 layers, H 4608, 32/16 heads
+x 128, MLP 36864) on 4 requests x 16384 tokens with 64 questions x 8 options
+each in the last 512 tokens; the default is the 9B workload above.
 """
 
 from __future__ import annotations
@@ -50,6 +54,21 @@ def synthetic_batch(vocab: int, seed: int = 0):
             req.append([(int(p), int(r.integers(0, vocab))) for p in pos[used:used + c]])
             used += int(c)
         options.append(req)
+    return lengths, ids, options
+
+
+def synthetic_batch_27b(vocab: int, seed: int = 0, requests: int = 4, length: int = 16384, questions: int = 64,
+                        per_question: int = 8):
+    """Long-context batch: `requests` x `length` tokens, `questions` x `per_question` options per request
+    at distinct positions of the last questions * per_question tokens."""
+    r = np.random.Generator(np.random.PCG64(seed))
+    lengths = [length] * requests
+    ids = [r.integers(0, vocab, length).tolist() for _ in range(requests)]
+    options = []
+    for n in lengths:
+        pos = r.permutation(np.arange(n - questions * per_question, n))
+        options.append([[(int(p), int(r.integers(0, vocab))) for p in pos[q * per_question:(q + 1) * per_question]]
+                        for q in range(questions)])
     return lengths, ids, options
 
 
@@ -129,13 +148,13 @@ def algorithmic_work(cfg, lengths: list[int]) -> dict[str, float]:
     }
 
 
-TRAFFIC_PROFILES = {"gate_up_proj": ROOT / "profiles" / "gate_up_gemm_traffic.md"}
+TRAFFIC_PROFILES = {("gemma2-9b", "gate_up_proj"): ROOT / "profiles" / "gate_up_gemm_traffic.md"}
 
 
-def measured_traffic(kernel: str) -> float | None:
+def measured_traffic(model: str, kernel: str) -> float | None:
     """HBM bytes per launch of `kernel` from its committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary
     (counters scaled by a plain-copy calibration), or None when no such summary exists."""
-    path = TRAFFIC_PROFILES.get(kernel)
+    path = TRAFFIC_PROFILES.get((model, kernel))
     if path is None or not path.exists():
         return None
     for line in path.read_text().splitlines():
@@ -191,8 +210,9 @@ def cpu_baseline(cfg, seconds_budget: float = 25.0, n: int = 2048) -> dict:
     sample_flops = n * replace(cfg, layers=layers).linear_flops_per_token() + replace(cfg, layers=layers).attention_flops([n])
     t = float(np.median(times))
     return {"flop_rate": sample_flops / t, "seconds": t, "runs": len(times), "threads": threads,
-            "sample": f"1 request x {n} tokens, 1 sliding + 1 global 9B-shaped layer + readout, numpy fp32 oracle, "
-                      f"median of {len(times)}; tokens/s extrapolated by FLOP count to the 42-layer batch"}
+            "sample": f"1 request x {n} tokens, 1 sliding + 1 global {cfg.name}-shaped layer + readout, numpy fp32 "
+                      f"oracle, median of {len(times)}; tokens/s extrapolated by FLOP count to the "
+                      f"{cfg.layers}-layer batch"}
 
 
 def main() -> None:
@@ -202,6 +222,7 @@ def main() -> None:
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--model", choices=("gemma2-9b", "gemma2-27b"), default="gemma2-9b")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one MI355X: the decision path runs on a single GPU (data parallel over requests "
@@ -213,12 +234,14 @@ def main() -> None:
     from deciax_amd import gemma
     from deciax_amd import kernels as K
 
-    cfg = gemma.CONFIGS["gemma2-9b"]
+    cfg = gemma.CONFIGS[args.model]
     t0 = time.time()
     weights = gemma.random_weights(cfg, seed=args.seed)
     torch.cuda.synchronize()
     print(f"# weights {weights.nbytes() / 1e9:.1f} GB in {time.time() - t0:.1f}s", file=sys.stderr, flush=True)
-    lengths, ids, options = synthetic_batch(cfg.vocab, seed=args.seed)
+    make = synthetic_batch if args.model == "gemma2-9b" else synthetic_batch_27b
+    lengths, ids, options = make(cfg.vocab, seed=args.seed)
+    n_questions = sum(len(q) for q in options)
     batch = gemma.pack_batch(ids, options)
     ws = gemma.Workspace(cfg, batch.rows, batch.vt_ld, weights.device)
     tokens = batch.rows
@@ -263,7 +286,7 @@ def main() -> None:
         "peak": PEAK_BF16 / 1e12,
         "unit": "TFLOP/s",
         "frac": round(dom.get("frac_bf16_peak", 0.0), 4),
-        "traffic": measured_traffic(dominant),
+        "traffic": measured_traffic(cfg.name, dominant),
         "algorithmic_flop_per_launch": work.get(dominant, 0.0),
     }
     attn_ms = sum(kern[k]["total_ms"] for k in kern if k.startswith("attention")) / args.steps
@@ -278,7 +301,7 @@ def main() -> None:
                "sample_seconds": round(cb["seconds"], 3), "extrapolated": True}
 
     result = {
-        "metric": "prefill tokens/s (9B-shaped decision forward, 1 GPU)",
+        "metric": f"prefill tokens/s ({'9B' if args.model == 'gemma2-9b' else '27B'}-shaped decision forward, 1 GPU)",
         "value": round(tokens / (ms * 1e-3), 1),
         "unit": "tokens/s",
         "n_gpus": 1,
@@ -290,11 +313,14 @@ def main() -> None:
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic (random-init weights, uniform-random token ids)",
-        "config": {"workload": "gemma2-9b-shaped decision forward, 42 layers, batch 16, lengths log-uniform "
-                               "[256, 16384] (seed 0), 8 questions x 2-8 options",
+        "config": {"workload": (f"gemma2-9b-shaped decision forward, 42 layers, batch 16, lengths log-uniform "
+                                f"[256, 16384] (seed {args.seed}), 8 questions x 2-8 options"
+                                if args.model == "gemma2-9b" else
+                                f"gemma2-27b-shaped decision forward, 46 layers, batch 4 x 16384 tokens (seed "
+                                f"{args.seed}), 64 questions x 8 options per request"),
                    "tokens_per_step": tokens, "requests": len(lengths), "lengths": lengths},
         "decisions_per_s": round(len(lengths) / (ms * 1e-3), 3),
-        "questions_per_s": round(len(lengths) * QUESTIONS / (ms * 1e-3), 2),
+        "questions_per_s": round(n_questions / (ms * 1e-3), 2),
         "tflops": round(total_flops / (ms * 1e-3) / 1e12, 2),
         "frac_bf16_peak": round(total_flops / (ms * 1e-3) / PEAK_BF16, 4),
         "attention": {"tflops": round(attn_flops / (attn_ms * 1e-3) / 1e12, 2),
