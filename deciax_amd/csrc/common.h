@@ -65,18 +65,13 @@ DX_DEVICE float wave_max(float v) {
   return v;
 }
 
-// tanh from the exponential identity tanh(y) = 1 - 2 / (1 + e^{2y}).
-// Absolute error is a few fp32 ulps of 1, far below bf16 resolution where it
-// is used (GELU-tanh epilogues, logit soft-capping).
-DX_DEVICE float tanh_exp(float y) {
-  const float e = fast_exp2(y * 2.8853900817779268f);  // 2 * log2(e)
-  return 1.0f - 2.0f * fast_rcp(1.0f + e);
-}
-
-// GELU with the tanh approximation: 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))).
+// GELU with the tanh approximation, 0.5 x (1 + tanh(y)), y = sqrt(2/pi) (x + 0.044715 x^3).
+// Since 1 + tanh(y) = 2 / (1 + e^{-2y}) this is x / (1 + 2^{-x (c1 + c2 x^2)}) with
+// c1 = 2 sqrt(2/pi) log2(e) and c2 = 0.044715 c1: one exp2 and one reciprocal, and no
+// cancellation for negative x (relative error about 1e-6 against the exact formula).
 DX_DEVICE float gelu_tanh(float x) {
-  const float inner = 0.7978845608028654f * (x + 0.044715f * x * x * x);
-  return 0.5f * x * (1.0f + tanh_exp(inner));
+  const float e = fast_exp2(x * __builtin_fmaf(x * x, -0.1029432395800235f, -2.302208198144325f));
+  return x * fast_rcp(1.0f + e);
 }
 
 // SiLU x * sigmoid(x).
