@@ -200,7 +200,7 @@ gemm_nt_kernel(const uint16_t *__restrict__ A, const uint16_t *__restrict__ B, v
   constexpr int NG = NC / 4;                           // chunk loads per k-step
   constexpr int GS = NM / NG;                          // MFMAs between two loads
   constexpr int W0 = (NC + 2) / 3, W1 = (NC + 1) / 3;  // writes per pre-barrier k-step
-  constexpr int R0 = NM / 4;                           // first fragment-read slot
+  constexpr int R0 = BM == 256 ? 6 : NM / 4;          // first fragment-read slot
   static_assert(GS >= 2 && W0 <= NM && R0 + NR <= NM, "region schedule");
 #define DX_REGION(nw, ng)                                                                          \
   do {                                                                                             \
@@ -463,8 +463,10 @@ hipError_t launch(const uint16_t *A, const uint16_t *B, void *C, long M, long N,
                   long ldc, int act, const QkvEpilogue &qe, hipStream_t s) {
   const long num_m = (M + BM - 1) / BM, num_n = N / BN;
   // Long K (activations streamed from HBM) keeps the register-staged path and its two tiles of
-  // latency slack; shorter K takes the direct-to-LDS path (measured on the 9B projections: gate|up
-  // +3%, down -1.5% with direct-to-LDS).
+  // latency slack; shorter K takes the direct-to-LDS path. Measured inside the 9B forward: gate|up +3%
+  // with direct-to-LDS, the down projection (K 14336) -1.3%. (Run alone on a fixed input, the down
+  // shape favours direct-to-LDS by 3%: its input, just written by gate|up, arrives with other cache
+  // state in the forward.)
   auto kern = K <= 8192 ? gemm_nt_kernel<BM, EPI, true> : gemm_nt_kernel<BM, EPI, false>;
   kern<<<dim3((unsigned)(num_m * num_n)), dim3(THREADS), 0, s>>>(A, B, C, (int)M, (int)N, (int)K, lda, ldb, ldc,
                                                                  act, qe);
