@@ -12,7 +12,10 @@ Differences, both for the varlen GPU forward:
     src/deciax/runtime/buckets.py) — `deciax_amd.gemma.pack_batch`;
   * each option is read at one position with one label token (the last token
     of its span and the first token of its id) instead of the Clef joint
-    schema head (src/deciax/models/clef/head.py:54-107, not part of this path).
+    schema head (src/deciax/models/clef/head.py:54-107).
+
+`head_inputs` lays encoded requests out for that joint head (`deciax_amd.clef_head`)
+as the reference's collate does (:140-182), padded to the batch maxima.
 """
 
 from __future__ import annotations
@@ -161,7 +164,7 @@ def encode(tokenizer: TokenizerLike, state: Any, questions: Mapping[str, Any], m
         fields.append(Field(qid, QTYPES[q["type"]], span, tuple(spans), tuple(ids), tuple(labels)))
 
     prefix = tok(f"<|im_start|>system\n{SYSTEM_PROMPT}<|im_end|>\n<|im_start|>user\nSTATE:\n")
-    suffix = tok("\n<|im_end|>\n<|im_start|>assistant\n\nJOINT SCHEMA DECISIONS:")
+    suffix = tok("\n<|im_end|>\n<|im_start|>assistant\n<think>\n\n</think>\n\nJOINT SCHEMA DECISIONS:")
     fixed = len(prefix) + len(schema) + len(suffix)
     if fixed > max_length:
         raise ValueError(f"schema requires {fixed} tokens before state; maximum is {max_length}")
@@ -175,6 +178,52 @@ def encode(tokenizer: TokenizerLike, state: Any, questions: Mapping[str, Any], m
     if vocab is not None and any(not 0 <= t < vocab for t in ids_all):
         raise ValueError("token id outside the model vocabulary")
     return Record(ids_all, shifted)
+
+
+def head_inputs(records: Sequence[Record], pad_id: int) -> dict[str, np.ndarray]:
+    """The Clef joint head's inputs for encoded requests, in the layout and under the names of
+    src/deciax/models/clef/input.py:140-182: options flat per request with the index of the field
+    that owns them, and `lexical_ids` holding every option's span tokens back to back (the
+    option's `lexical_spans` range in it). Shapes are the batch maxima: the reference rounds them
+    up to power-of-two buckets so jit compiles once per bucket, and its padding is masked, so that
+    rounding changes no output (src/deciax/runtime/buckets.py:1-3)."""
+    if not records:
+        raise ValueError("no records")
+    b = len(records)
+    s = max(len(r.ids) for r in records)
+    q = max(len(r.fields) for r in records)
+    o = max(sum(len(f.option_ids) for f in r.fields) for r in records)
+    lex = [[t for f in r.fields for lo, hi in f.option_spans for t in r.ids[lo:hi]] for r in records]
+    out = {
+        "lexical_ids": np.full((b, max(1, max(map(len, lex)))), pad_id, np.int32),
+        "lexical_spans": np.zeros((b, o, 2), np.int32),
+        "input_ids": np.full((b, s), pad_id, np.int32),
+        "mask": np.zeros((b, s), bool),
+        "question_spans": np.zeros((b, q, 2), np.int32),
+        "question_mask": np.zeros((b, q), bool),
+        "types": np.zeros((b, q), np.int32),
+        "option_spans": np.zeros((b, o, 2), np.int32),
+        "option_mask": np.zeros((b, o), bool),
+        "option_field": np.zeros((b, o), np.int32),
+    }
+    for i, r in enumerate(records):
+        out["input_ids"][i, :len(r.ids)] = r.ids
+        out["mask"][i, :len(r.ids)] = True
+        out["lexical_ids"][i, :len(lex[i])] = lex[i]
+        opt = 0      # flat option index in this request
+        cursor = 0   # next free position in lexical_ids[i]
+        for k, f in enumerate(r.fields):
+            out["question_spans"][i, k] = f.span
+            out["question_mask"][i, k] = True
+            out["types"][i, k] = f.kind
+            for lo, hi in f.option_spans:
+                out["option_spans"][i, opt] = (lo, hi)
+                out["option_mask"][i, opt] = True
+                out["option_field"][i, opt] = k
+                out["lexical_spans"][i, opt] = (cursor, cursor + hi - lo)
+                cursor += hi - lo
+                opt += 1
+    return out
 
 
 def readout_layout(records: Sequence[Record]) -> list[list[list[tuple[int, int]]]]:

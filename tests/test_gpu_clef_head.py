@@ -123,3 +123,41 @@ def test_head_matches_oracle_random_shapes(shape: dict) -> None:
     live = a["option_mask"]
     np.testing.assert_allclose(got[live], want[live], atol=2e-5, rtol=2e-4)
     assert (got[~live] == np.float32(-1e9)).all()
+
+
+def test_encoded_requests_through_head() -> None:
+    """Requests encoded by deciax_amd.schema, laid out by `head_inputs` (the reference's collate,
+    src/deciax/models/clef/input.py:140-182), with lexical vectors gathered on the GPU: the head's
+    logits match the oracle fed the same arrays, and decode to the same answers."""
+    import torch
+
+    from deciax_amd import clef_head
+    from deciax_amd.schema import ByteTokenizer, decode, encode, head_inputs
+    from oracle import clef_head as oc
+
+    say("clef head: encoded requests")
+    tok = ByteTokenizer()
+    questions = {"mood": {"type": "choice", "criteria": {"pos": "positive", "neg": "negative", "mix": None}},
+                 "late": {"type": "noul"}, "stars": {"type": "score", "criteria": ["bad", "ok", "good"]}}
+    records = [encode(tok, s, questions, 2048) for s in ("the parcel came late", {"ticket": 7, "text": "great"})]
+    a = head_inputs(records, tok.pad_token_id)
+    r = rng(11)
+    batch, seq = a["input_ids"].shape
+    hidden_dim = 64
+    p, _, _, _ = _random_case(5, batch=batch, seq=seq, hidden=hidden_dim, width=32, ff=48, nq=3, no=8, ntypes=3,
+                              routing_layers=1, layers=2)
+    hidden = r.normal(size=(batch, seq, hidden_dim)).astype(np.float32)
+    embedding = r.normal(size=(tok.vocab, hidden_dim)).astype(np.float32)
+    lexical = clef_head.lexical_vectors(torch.as_tensor(embedding).cuda(), a["lexical_ids"], a["lexical_spans"])
+    want_lex = oc.means(embedding[a["lexical_ids"]], a["lexical_spans"])
+    np.testing.assert_allclose(lexical.cpu().numpy(), want_lex, atol=1e-5, rtol=1e-5)
+    got = clef_head.forward(_dev_params(p), hidden, lexical, a, heads=4, routing_layers=1, layers=2).cpu().numpy()
+    want = oc.forward(p, hidden, want_lex, a, heads=4, routing_layers=1, layers=2)
+    live = a["option_mask"]
+    np.testing.assert_allclose(got[live], want[live], atol=2e-5, rtol=2e-4)
+    for i, record in enumerate(records):
+        n = int(live[i].sum())
+        ours, theirs = decode(record, got[i, :n], questions, "m"), decode(record, want[i, :n], questions, "m")
+        assert ours["answers"]["mood"]["choice"] == theirs["answers"]["mood"]["choice"]
+        assert ours["answers"]["late"]["noul"] == pytest.approx(theirs["answers"]["late"]["noul"], abs=2e-4)
+        assert ours["answers"]["stars"]["score"] == pytest.approx(theirs["answers"]["stars"]["score"], abs=2e-4)

@@ -200,6 +200,68 @@ def test_truncation_keeps_schema_complete(tokenizer: Any) -> None:
         encode(tokenizer, "", q, len(fixed.ids) - 1)
 
 
+def test_prompt_text_kat() -> None:
+    """The serialised prompt is part of the trained model's input contract
+    (src/deciax/models/clef/input.py:98-125). With the byte tokenizer the ids decode back to the
+    text, which must equal this worked example character for character; the question span
+    covers the instruction and each option span its JSON semantics."""
+    from deciax_amd.schema import SYSTEM_PROMPT, ByteTokenizer, encode
+
+    tok = ByteTokenizer()
+    record = encode(tok, {"b": 2, "a": "x"}, {"q": {"type": "noul"}}, 4096)
+    text = bytes(t - tok.offset for t in record.ids).decode("utf-8")
+    yes = '{"description":"The proposition is true or the answer is yes.","option_id":"true"}'
+    no = '{"description":"The proposition is false or the answer is no.","option_id":"false"}'
+    want = ("<|im_start|>system\n" + SYSTEM_PROMPT + "<|im_end|>\n<|im_start|>user\nSTATE:\n"
+            '{"a":"x","b":2}'
+            "\n\nSCHEMA FIELDS:\n"
+            "\nFIELD 1\nID: q\nTYPE: noul\nINSTRUCTION: q\nALLOWED OPTIONS:\n"
+            "OPTION 1: " + yes + "\nOPTION 2: " + no + "\nEND FIELD\n"
+            "\n<|im_end|>\n<|im_start|>assistant\n<think>\n\n</think>\n\nJOINT SCHEMA DECISIONS:")
+    assert text == want
+    assert SYSTEM_PROMPT == ("Read the complete state and schema. Decide every field jointly. Each answer must be "
+                             "exactly one of that field's allowed options.")
+
+    def piece(span: tuple[int, int]) -> str:
+        return bytes(t - tok.offset for t in record.ids[span[0]:span[1]]).decode("utf-8")
+
+    (field,) = record.fields
+    assert piece(field.span) == "q"
+    assert [piece(s) for s in field.option_spans] == [yes, no]
+
+
+def test_head_inputs_layout(tokenizer: Any) -> None:
+    """Joint-head inputs in the layout of src/deciax/models/clef/input.py:140-182: options flat
+    with their owning field, lexical_ids holding each option's span tokens back to back."""
+    from deciax_amd.schema import encode, head_inputs
+
+    questions2 = {"only": {"type": "choice", "criteria": {"b": "world", "a": "hello"}}}
+    records = [encode(tokenizer, "hello world", QUESTIONS, 512), encode(tokenizer, "hello", questions2, 512)]
+    a = head_inputs(records, pad_id=tokenizer.pad_token_id)
+    assert a["input_ids"].shape == a["mask"].shape == (2, max(len(r.ids) for r in records))
+    assert a["question_spans"].shape == (2, 3, 2) and a["option_spans"].shape == (2, 7, 2)
+    assert a["mask"].sum(1).tolist() == [len(r.ids) for r in records]
+    assert a["question_mask"].tolist() == [[True] * 3, [True, False, False]]
+    assert a["types"][0].tolist() == [1, 0, 2] and a["types"][1, 0] == 1
+    assert a["option_mask"].sum(1).tolist() == [7, 2]
+    assert a["option_field"][0].tolist() == [0, 0, 1, 1, 2, 2, 2]
+    for i, r in enumerate(records):
+        assert a["input_ids"][i, :len(r.ids)].tolist() == list(r.ids)
+        assert (a["input_ids"][i, len(r.ids):] == tokenizer.pad_token_id).all()
+        flat = [(f, s) for f in r.fields for s in f.option_spans]
+        cursor = 0
+        for o, (f, (lo, hi)) in enumerate(flat):
+            assert tuple(a["option_spans"][i, o]) == (lo, hi)
+            l0, l1 = a["lexical_spans"][i, o]
+            assert (l0, l1) == (cursor, cursor + hi - lo)
+            assert a["lexical_ids"][i, l0:l1].tolist() == list(r.ids[lo:hi])
+            cursor = l1
+        for k, f in enumerate(r.fields):
+            assert tuple(a["question_spans"][i, k]) == f.span
+    with pytest.raises(ValueError):
+        head_inputs([], 0)
+
+
 @pytest.mark.parametrize("questions", [
     {},
     {"q": {"type": []}},
