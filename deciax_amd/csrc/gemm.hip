@@ -50,6 +50,11 @@
 
 namespace {
 
+template <bool B>
+struct Flag {
+  static constexpr bool value = B;
+};
+
 template <int I>
 struct Int {
   static constexpr int value = I;
@@ -187,11 +192,14 @@ gemm_nt_kernel(const uint16_t *__restrict__ A, const uint16_t *__restrict__ B, v
     for (int j = 0; j < TN; ++j)
       fb[j] = as_bf16x8(*reinterpret_cast<const u32x4 *>(sb + swz(wn * (BN / 2) + j * 32 + lrow, c)));
   };
+  // B as the first MFMA operand: block (i, j) holds the transposed product, so lane (lrow, lhalf) has
+  // register r at row i * 32 + lrow and column j * 32 + (r >> 2) * 8 + lhalf * 4 + (r & 3) of the wave's
+  // quadrant, four consecutive columns per register group (8-byte staging writes, 16-byte fp32 stores)
   auto mm = [&](const bf16x8 *fa, const bf16x8 *fb) {
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
-      for (int j = 0; j < TN; ++j) acc[i][j] = mfma32(fa[i], fb[j], acc[i][j]);
+      for (int j = 0; j < TN; ++j) acc[i][j] = mfma32(fb[j], fa[i], acc[i][j]);
   };
 
   // One k-step region: NM MFMAs; nw LDS writes in the first slots, one load after every GS
@@ -330,15 +338,19 @@ gemm_nt_kernel(const uint16_t *__restrict__ A, const uint16_t *__restrict__ B, v
   if constexpr (EPI == EPI_F32) {
     float *Cf = reinterpret_cast<float *>(C);
 #pragma unroll
-    for (int i = 0; i < TM; ++i)
+    for (int i = 0; i < TM; ++i) {
+      const int row = m0 + wm * (BM / 2) + i * 32 + lrow;
+      if (row < M) {
 #pragma unroll
-      for (int j = 0; j < TN; ++j)
+        for (int j = 0; j < TN; ++j)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int row = m0 + wm * (BM / 2) + i * 32 + (r >> 2) * 8 + lhalf * 4 + (r & 3);
-          const int col = n0 + wn * (BN / 2) + j * 32 + lrow;
-          if (row < M) Cf[(long)row * ldc + col] = acc[i][j][r];
-        }
+          for (int q = 0; q < 4; ++q) {
+            const int col = n0 + wn * (BN / 2) + j * 32 + q * 8 + lhalf * 4;
+            const floatx4 v = {acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+            *reinterpret_cast<floatx4 *>(Cf + (long)row * ldc + col) = v;
+          }
+      }
+    }
   } else {
     // Stage the bf16 tile through LDS, then store 16-byte row chunks. A QKV tile made only of v
     // columns is staged transposed ([col][row], pitch BM + 8): its stores walk V^T rows.
@@ -346,43 +358,60 @@ gemm_nt_kernel(const uint16_t *__restrict__ A, const uint16_t *__restrict__ B, v
     if (vt_tile) {
       constexpr int TP = BM + 8;
 #pragma unroll
-      for (int i = 0; i < TM; ++i)
+      for (int i = 0; i < TM; ++i) {
+        const int row = wm * (BM / 2) + i * 32 + lrow;
 #pragma unroll
-        for (int r = 0; r < 16; r += 4) {
-          const int row = wm * (BM / 2) + i * 32 + (r >> 2) * 8 + lhalf * 4;
+        for (int j = 0; j < TN; ++j)
 #pragma unroll
-          for (int j = 0; j < TN; ++j) {
-            const int col = wn * (BN / 2) + j * 32 + lrow;
-            u32x2 w;
-            w[0] = pack_bf2(acc[i][j][r], acc[i][j][r + 1]);
-            w[1] = pack_bf2(acc[i][j][r + 2], acc[i][j][r + 3]);
-            *reinterpret_cast<u32x2 *>(smem + col * TP + row) = w;
+          for (int r = 0; r < 16; ++r) {
+            const int col = wn * (BN / 2) + j * 32 + (r >> 2) * 8 + lhalf * 4 + (r & 3);
+            smem[col * TP + row] = f2bf(acc[i][j][r]);
           }
-        }
-    } else
-#pragma unroll
-    for (int i = 0; i < TM; ++i)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int row = wm * (BM / 2) + i * 32 + (r >> 2) * 8 + lhalf * 4 + (r & 3);
-        if constexpr (EPI == EPI_BF16 || EPI == EPI_QKV) {
-#pragma unroll
-          for (int j = 0; j < TN; ++j) {
-            const int col = wn * (BN / 2) + j * 32 + lrow;
-            smem[row * OUT_PITCH + col] = f2bf(acc[i][j][r]);
-          }
-        } else {
-          // Wave columns [0, BN/4) are gate, [BN/4, BN/2) the matching up.
-#pragma unroll
-          for (int j = 0; j < TN / 2; ++j) {
-            const float g = round_bf(acc[i][j][r]);
-            const float u = round_bf(acc[i][j + TN / 2][r]);
-            const float a = round_bf(act == DX_ACT_SILU ? silu(g) : gelu_tanh(g));
-            const int col = wn * (BN / 4) + j * 32 + lrow;
-            smem[row * OUT_PITCH + col] = f2bf(a * u);
-          }
-        }
       }
+    } else if constexpr (EPI == EPI_BF16 || EPI == EPI_QKV) {
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        const int row = wm * (BM / 2) + i * 32 + lrow;
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const int col = wn * (BN / 2) + j * 32 + q * 8 + lhalf * 4;
+            u32x2 w;
+            w[0] = pack_bf2(acc[i][j][4 * q], acc[i][j][4 * q + 1]);
+            w[1] = pack_bf2(acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]);
+            *reinterpret_cast<u32x2 *>(smem + row * OUT_PITCH + col) = w;
+          }
+      }
+    } else {
+      // Wave columns [0, BN/4) are gate, [BN/4, BN/2) the matching up: blocks j and j + TN/2 of the same
+      // lane. The activation is chosen once for the whole loop.
+      auto gated = [&](auto silu_c) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+          const int row = wm * (BM / 2) + i * 32 + lrow;
+#pragma unroll
+          for (int j = 0; j < TN / 2; ++j)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              float o[4];
+#pragma unroll
+              for (int e = 0; e < 4; ++e) {
+                const float g = round_bf(acc[i][j][4 * q + e]);
+                const float u = round_bf(acc[i][j + TN / 2][4 * q + e]);
+                o[e] = round_bf(decltype(silu_c)::value ? silu(g) : gelu_tanh(g)) * u;
+              }
+              const int col = wn * (BN / 4) + j * 32 + q * 8 + lhalf * 4;
+              u32x2 w;
+              w[0] = pack_bf2(o[0], o[1]);
+              w[1] = pack_bf2(o[2], o[3]);
+              *reinterpret_cast<u32x2 *>(smem + row * OUT_PITCH + col) = w;
+            }
+        }
+      };
+      if (act == DX_ACT_SILU) gated(Flag<true>());
+      else gated(Flag<false>());
+    }
     __syncthreads();
     uint16_t *Cb = reinterpret_cast<uint16_t *>(C);
     if constexpr (EPI == EPI_QKV) {
