@@ -315,3 +315,16 @@ def test_config_flop_counts() -> None:
     one = replace(c, layers=1, window=0)
     assert one.attention_flops([2048] * 8) == pytest.approx(2.750e11, rel=1e-3)
     assert c.query_scale == 1 / 16 and CONFIGS["gemma2-27b"].query_scale == pytest.approx(1 / 12)
+
+
+def test_bench_refuses_several_gpus() -> None:
+    """bench.py measures one MI355X: --gpus above 1 exits with a message before touching a GPU."""
+    import subprocess
+    import sys
+    from pathlib import Path
+
+    root = Path(__file__).resolve().parents[1]
+    res = subprocess.run([sys.executable, str(root / "bench.py"), "--gpus", "2"], capture_output=True, text=True,
+                         timeout=120, cwd=root)
+    assert res.returncode == 2
+    assert "--gpus 1" in res.stderr and res.stdout == ""
