@@ -209,3 +209,43 @@ def test_decide_end_to_end() -> None:
     assert single["answers"]["sentiment"] == out[0]["answers"]["sentiment"]
     with pytest.raises(ValueError):
         d.decide("x", {})
+
+
+@pytest.mark.parametrize("model", ["gemma2-9b", "gemma2-27b"])
+def test_full_size_batch_order_invariance(model: str) -> None:
+    """The benchmark's batches at full size (9B: 16 requests, 70471 tokens; 27B: 4 x 16384 tokens)
+    through all layers: rows are independent in every GEMM, norm and the readout, and attention is
+    independent per request, so each request's logits and probabilities must be bit-identical when
+    the batch runs in reverse order. This checks the varlen bookkeeping (positions, V^T columns,
+    readout gathers) at sizes the oracle cannot reach; every question's probabilities also sum to 1."""
+    import bench
+    from deciax_amd import gemma
+
+    cfg = gemma.CONFIGS[model]
+    say(f"full-size batch order invariance {model}")
+    make = bench.synthetic_batch if model == "gemma2-9b" else bench.synthetic_batch_27b
+    lengths, ids, options = make(cfg.vocab, seed=0)
+    w = gemma.random_weights(cfg, seed=0)
+
+    def run(order: list[int]) -> list[tuple[np.ndarray, np.ndarray]]:
+        batch = gemma.pack_batch([ids[i] for i in order], [options[i] for i in order])
+        logits, probs = gemma.forward(w, batch, gemma.Workspace(cfg, batch.rows, batch.vt_ld, w.device))
+        logits, probs = logits.cpu().numpy(), probs.cpu().numpy()
+        out, offset = {}, 0
+        for i in order:
+            n = sum(len(q) for q in options[i])
+            out[i] = (logits[offset:offset + n], probs[offset:offset + n])
+            offset += n
+        assert offset == len(logits)
+        return out
+
+    forward = run(list(range(len(lengths))))
+    backward = run(list(reversed(range(len(lengths)))))
+    for i in range(len(lengths)):
+        assert np.array_equal(forward[i][0], backward[i][0]), f"request {i}: logits depend on batch order"
+        assert np.array_equal(forward[i][1], backward[i][1]), f"request {i}: probabilities depend on batch order"
+        assert np.isfinite(forward[i][0]).all()
+        offset = 0
+        for q in options[i]:
+            assert abs(float(forward[i][1][offset:offset + len(q)].sum()) - 1.0) < 1e-5
+            offset += len(q)
