@@ -77,7 +77,9 @@ def _check(probs: np.ndarray, weights_np, config, batch) -> None:
                 assert np.argmax(probs[a:b]) == np.argmax(truth[a:b])
 
 
-@pytest.mark.parametrize("lengths", [[37, 200, 129, 64], [300]])
+@pytest.mark.parametrize("lengths", [[37, 200, 129, 64], [300],
+                                     [1, 2, 63, 64, 65, 127, 128, 129],  # tile, window and query-block edges
+                                     [1]])
 def test_tiny_forward_matches_oracle(lengths: list[int]) -> None:
     import torch
 
