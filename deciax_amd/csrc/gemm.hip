@@ -22,13 +22,13 @@
 // need.
 //
 // Direct-to-LDS. Buffer loads write the LDS tile themselves (buffer_load ... lds),
-// so there are no staging registers and no LDS writes. A stage is refilled as soon
-// as the barrier frees it: part of the loads of the tile after next follow the
-// barrier, the rest go in the next iteration's first k-step (gated projection: half
-// and half) or its first two k-steps (spread evenly, other epilogues). Issue, not
-// completion, is what loads cost here: with no loads at all the same loop runs at
-// the chip's power-limited MFMA rate, while waiting for their completion costs
-// nothing measurable.
+// so there are no staging registers and no LDS writes. 256-row tiles keep A in a
+// ring of three stages and B in a ring of two (the whole 160 KB): A's loads can then
+// run a full iteration ahead, and every k-step carries the same 4 loads per wave,
+// one per 4 MFMAs. 128-row tiles use two stages of both. The loads are what bounds
+// this loop: without them it runs at 83 % of the clock's MFMA peak, with them at
+// about 70 %, and it is neither their latency nor their rate at the address unit
+// (both measured).
 //
 // LDS layout: row-major [rows][64] bf16, 16-byte chunk c of row r stored at
 // chunk position c ^ ((r >> 1) & 7): a 32-lane fragment read touches 32 rows
@@ -112,7 +112,10 @@ gemm_nt_kernel(const uint16_t *__restrict__ A, const uint16_t *__restrict__ B, v
   static_assert(NC % 4 == 0 && NC % AC == 0, "chunk schedule");
   constexpr int OUT_W = EPI == EPI_GATED ? BN / 2 : BN;
   constexpr int OUT_PITCH = OUT_W + 8;
-  constexpr int SMEM = (2 * STAGE > BM * OUT_PITCH) ? 2 * STAGE : BM * OUT_PITCH;
+  // 256-row direct-to-LDS tiles use a ring of 3 A and 2 B stages (5 x 32 KB = the whole 160 KB)
+  constexpr bool RING = DTL && BM == 256;
+  constexpr int OPERANDS = RING ? 5 * BM * BK : 2 * STAGE;
+  constexpr int SMEM = (OPERANDS > BM * OUT_PITCH) ? OPERANDS : BM * OUT_PITCH;
   __shared__ __attribute__((aligned(1024))) uint16_t smem[SMEM];
 
   const int num_m = (M + BM - 1) / BM, num_n = N / BN;
@@ -221,16 +224,107 @@ gemm_nt_kernel(const uint16_t *__restrict__ A, const uint16_t *__restrict__ B, v
   } while (0)
 
   const int KT = K / BK;
-  if constexpr (DTL) {
-    // The NI loads of a tile go out P3 after the barrier that frees their stage, P0 in the next k-step
-    // and P1 in the one after, at evenly spaced MFMA slots; fragment reads take slots DR0 on. With 256-row
-    // tiles whose weight stays cache-resident (every epilogue but the gated one) the loads are spread
-    // over three k-steps, so the address unit is never asked for one load per two MFMAs; the gated
-    // projection streams its weight from HBM and keeps two k-steps of latency slack instead (measured:
-    // o +3%, qkv +1%, gate|up -2% when spread).
-    constexpr bool SPREAD = BM == 256 && EPI != EPI_GATED;
-    constexpr int P3 = SPREAD ? 6 : NI / 2, P0 = SPREAD ? 6 : NI - NI / 2, P1 = NI - P3 - P0;
-    constexpr int DR0 = BM == 256 ? 6 : R0;
+  if constexpr (RING) {
+    // A tile T goes to A stage T % 3, free once the barrier of iteration T - 3 has passed; its 8 loads
+    // per wave go out in k-steps 0 / 1 / 2 of iteration T - 2 (2 / 2 / 4), a full iteration or more
+    // before use. B tile T goes to B stage T % 2, free after the barrier of iteration T - 2; 4 loads
+    // follow that barrier and 2 / 2 go in k-steps 0 / 1 of iteration T - 1. Every k-step thus
+    // carries 4 loads per wave, one per 4 MFMAs (measured against the two-stage ring: +2-5% on the
+    // 9B and 27B q|k|v, o and gate|up shapes, bit-identical results).
+    static_assert(AI == 8 && BI == 8, "ring schedule: 8 A and 8 B instructions per wave");
+    constexpr int RS = BM * BK;  // elements per stage (A or B)
+    auto la = [&](int kt, int sa, int j0, int j1) __attribute__((always_inline)) {
+#pragma unroll
+      for (int j = j0; j < j1; ++j) lds_load16(ra, smem + sa * RS + (wave * AI + j) * 512, aoff[j], kt * BK * 2);
+    };
+    auto lb = [&](int kt, int sb, int j0, int j1) __attribute__((always_inline)) {
+#pragma unroll
+      for (int j = j0; j < j1; ++j)
+        lds_load16(rb, smem + (3 + sb) * RS + (wave * BI + j) * 512, boff[j], kt * BK * 2);
+    };
+    auto rdr = [&](bf16x8 *fa, bf16x8 *fb, int sa, int sb, int ks) __attribute__((always_inline)) {
+      const uint16_t *pa = smem + sa * RS;
+      const uint16_t *pb = smem + (3 + sb) * RS;
+      const int c = ks * 2 + lhalf;
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+        fa[i] = as_bf16x8(*reinterpret_cast<const u32x4 *>(pa + swz(wm * (BM / 2) + i * 32 + lrow, c)));
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+        fb[j] = as_bf16x8(*reinterpret_cast<const u32x4 *>(pb + swz(wn * (BN / 2) + j * 32 + lrow, c)));
+    };
+    constexpr int DR0 = 6;  // fragment reads in MFMA slots 6..13
+    static_assert(DR0 + NR <= NM, "ring region schedule");
+#define DX_RREGION()                                                                               \
+  do {                                                                                             \
+    _Pragma("unroll") for (int t = 0; t < NM; ++t) {                                               \
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                                           \
+      if (t % 4 == 0) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);                           \
+      if (t >= DR0 && t - DR0 < NR) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);             \
+    }                                                                                              \
+  } while (0)
+    auto cl = [&](int t) { return min(t, KT - 1); };  // past the end: reload the last tile into a freed stage
+    // tiles 0 and 1 of A, tile 0 of B and the loads of B tile 1 that precede iteration 0
+    la(0, 0, 0, 8);
+    lb(0, 0, 0, 8);
+    la(cl(1), 1, 0, 8);
+    lb(cl(1), 1, 0, 4);
+    asm volatile("s_waitcnt vmcnt(12)" ::: "memory");
+    __syncthreads();
+    rdr(fa0, fb0, 0, 0, 0);
+    // Iteration kt (q = kt % 6 at compile time, so every stage is an immediate).
+    auto iteration = [&](const int kt, auto qc) __attribute__((always_inline)) {
+      constexpr int q = decltype(qc)::value;
+      constexpr int sa = q % 3, sb = q % 2, sa1 = (q + 1) % 3, sb1 = (q + 1) % 2, sa2 = (q + 2) % 3;
+      __builtin_amdgcn_sched_barrier(0);
+      lb(cl(kt + 1), sb1, 4, 6);
+      la(cl(kt + 2), sa2, 0, 2);
+      rdr(fa1, fb1, sa, sb, 1);
+      mm(fa0, fb0);
+      DX_RREGION();
+      __builtin_amdgcn_sched_barrier(0);
+      lb(cl(kt + 1), sb1, 6, 8);
+      la(cl(kt + 2), sa2, 2, 4);
+      rdr(fa0, fb0, sa, sb, 2);
+      mm(fa1, fb1);
+      DX_RREGION();
+      __builtin_amdgcn_sched_barrier(0);
+      la(cl(kt + 2), sa2, 4, 8);
+      rdr(fa1, fb1, sa, sb, 3);
+      mm(fa0, fb0);
+      DX_RREGION();
+      __builtin_amdgcn_sched_barrier(0);
+      // A and B of tile kt + 1 have landed (only this k-step's 4 loads may be younger), and every wave is
+      // done with tile kt, whose stages the next loads refill
+      asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)" ::: "memory");
+      __builtin_amdgcn_s_barrier();
+      __builtin_amdgcn_sched_barrier(0);
+      lb(cl(kt + 2), sb, 0, 4);
+      rdr(fa0, fb0, sa1, sb1, 0);
+      mm(fa1, fb1);
+      DX_RREGION();
+      __builtin_amdgcn_sched_barrier(0);
+    };
+    int kt = 0;
+    for (; kt + 5 < KT; kt += 6) {
+      iteration(kt, Int<0>());
+      iteration(kt + 1, Int<1>());
+      iteration(kt + 2, Int<2>());
+      iteration(kt + 3, Int<3>());
+      iteration(kt + 4, Int<4>());
+      iteration(kt + 5, Int<5>());
+    }
+    if (kt < KT) iteration(kt, Int<0>());
+    if (kt + 1 < KT) iteration(kt + 1, Int<1>());
+    if (kt + 2 < KT) iteration(kt + 2, Int<2>());
+    if (kt + 3 < KT) iteration(kt + 3, Int<3>());
+    if (kt + 4 < KT) iteration(kt + 4, Int<4>());
+#undef DX_RREGION
+  } else if constexpr (DTL) {
+    // Two stages (128-row tiles): the NI loads of a tile go out half (P3) after the barrier that frees
+    // their stage and half (P0) in the next k-step, at evenly spaced MFMA slots.
+    constexpr int P3 = NI / 2, P0 = NI - NI / 2, P1 = NI - P3 - P0;
+    constexpr int DR0 = R0;
     static_assert(P1 >= 0 && DR0 + NR <= NM, "load schedule");
 #define DX_DREGION(nl)                                                                             \
   do {                                                                                             \
