@@ -6,7 +6,7 @@
 // wave owns a BM/2 x 128 quadrant in 32x32x16 MFMA blocks with fp32
 // accumulators (a single wave saturates the matrix core with this shape).
 //
-// Two data paths, chosen per shape (K <= 8192 takes the second):
+// Two data paths (256-row tiles, and 128-row tiles with K <= 8192, take the second):
 //
 // Register-staged. Per thread and K tile: 16-byte chunks arrive through buffer loads
 // (the resource is based at the tile origin, so rows past M read as zero and
@@ -585,12 +585,11 @@ template <int BM, int EPI>
 hipError_t launch(const uint16_t *A, const uint16_t *B, void *C, long M, long N, long K, long lda, long ldb,
                   long ldc, int act, const QkvEpilogue &qe, hipStream_t s) {
   const long num_m = (M + BM - 1) / BM, num_n = N / BN;
-  // Long K (activations streamed from HBM) keeps the register-staged path and its two tiles of
-  // latency slack; shorter K takes the direct-to-LDS path. Measured inside the 9B forward: gate|up +3%
-  // with direct-to-LDS, the down projection (K 14336) -1.3%. (Run alone on a fixed input, the down
-  // shape favours direct-to-LDS by 3%: its input, just written by gate|up, arrives with other cache
-  // state in the forward.)
-  auto kern = K <= 8192 ? gemm_nt_kernel<BM, EPI, true> : gemm_nt_kernel<BM, EPI, false>;
+  // 256-row tiles always take the direct-to-LDS ring: its A stages give long-K shapes the latency slack
+  // (against the register-staged path: down K 14336 +3-8 % alone and -0.8 % step time in the 9B
+  // forward, K 36864 +4.5 %, 1344- and 448-tile down shapes +2.5 % / +1 %). 128-row tiles (M <= 1024)
+  // have two stages only, so long K keeps the register-staged path and its two tiles of slack there.
+  auto kern = (BM == 256 || K <= 8192) ? gemm_nt_kernel<BM, EPI, true> : gemm_nt_kernel<BM, EPI, false>;
   kern<<<dim3((unsigned)(num_m * num_n)), dim3(THREADS), 0, s>>>(A, B, C, (int)M, (int)N, (int)K, lda, ldb, ldc,
                                                                  act, qe);
   return hipGetLastError();
