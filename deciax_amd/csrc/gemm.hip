@@ -116,6 +116,10 @@ gemm_nt_kernel(const uint16_t *__restrict__ A, const uint16_t *__restrict__ B, v
   constexpr bool RING = DTL && BM == 256;
   constexpr int OPERANDS = RING ? 5 * BM * BK : 2 * STAGE;
   constexpr int SMEM = (OPERANDS > BM * OUT_PITCH) ? OPERANDS : BM * OUT_PITCH;
+  // q|k|v epilogue: each tile row's clamped RoPE position and V^T column (2 BM int32) sit in LDS above
+  // the staged tile (row-major BM x OUT_PITCH, or transposed BN x (BM + 8) for a V^T tile)
+  constexpr int ROW_INFO = BN * (BM + 8) > BM * OUT_PITCH ? BN * (BM + 8) : BM * OUT_PITCH;
+  static_assert(EPI != EPI_QKV || ROW_INFO + 4 * BM <= SMEM, "q|k|v row info fits the LDS");
   __shared__ __attribute__((aligned(1024))) uint16_t smem[SMEM];
 
   const int num_m = (M + BM - 1) / BM, num_n = N / BN;
@@ -449,6 +453,13 @@ gemm_nt_kernel(const uint16_t *__restrict__ A, const uint16_t *__restrict__ B, v
     // Stage the bf16 tile through LDS, then store 16-byte row chunks. A QKV tile made only of v
     // columns is staged transposed ([col][row], pitch BM + 8): its stores walk V^T rows.
     const bool vt_tile = EPI == EPI_QKV && n0 >= qe.qk_cols;
+    int *const row_pos = reinterpret_cast<int *>(smem + ROW_INFO), *const row_col = row_pos + BM;
+    if (EPI == EPI_QKV && tid < BM) {
+      // one global load per row, issued before the staging so its latency hides behind it
+      const bool live = m0 + tid < M;
+      row_pos[tid] = live ? min(max(qe.pos[m0 + tid], 0), qe.max_pos - 1) : 0;
+      row_col[tid] = live ? qe.vt_col[m0 + tid] : 0;
+    }
     if (vt_tile) {
       constexpr int TP = BM + 8;
 #pragma unroll
@@ -509,34 +520,48 @@ gemm_nt_kernel(const uint16_t *__restrict__ A, const uint16_t *__restrict__ B, v
     __syncthreads();
     uint16_t *Cb = reinterpret_cast<uint16_t *>(C);
     if constexpr (EPI == EPI_QKV) {
-      // q / k heads (head columns below qk_cols): item = (row, head, 8 rotary pairs j0..j0+7)
+      // q / k heads (head columns below qk_cols): thread t rotates the pairs (j0 .. j0 + 7, + half) of one
+      // head in tile rows t / 16 + 16 i. The cos / sin rows of 8 such rows are all requested before the
+      // first is used, so the table reads cost one round trip per 8 rows.
       const int d = qe.d, half = d / 2, per_head = d / 16;
-      for (int idx = vt_tile ? BM * (BN / 16) : tid; idx < BM * (BN / 16); idx += THREADS) {
-        const int row = idx / (BN / 16), rem = idx % (BN / 16);
-        const int j0 = (rem % per_head) * 8, c1 = (rem / per_head) * d + j0;
-        if (m0 + row >= M || n0 + c1 >= qe.qk_cols) continue;
-        const int p = min(max(qe.pos[m0 + row], 0), qe.max_pos - 1);
-        const u32x4 a = *reinterpret_cast<const u32x4 *>(smem + row * OUT_PITCH + c1);
-        const u32x4 b = *reinterpret_cast<const u32x4 *>(smem + row * OUT_PITCH + c1 + half);
-        const u32x4 cs = *reinterpret_cast<const u32x4 *>(qe.cos + (long)p * half + j0);
-        const u32x4 sn = *reinterpret_cast<const u32x4 *>(qe.sin + (long)p * half + j0);
-        u32x4 o1, o2;
+      const int rem = tid % (BN / 16), j0 = (rem % per_head) * 8, c1 = (rem / per_head) * d + j0;
+      if (!vt_tile && n0 + c1 < qe.qk_cols) {
+        constexpr int RSTEP = THREADS / (BN / 16), NR = BM / RSTEP, BATCH = 8;
+        static_assert(NR % BATCH == 0, "rotary row batches");
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          float r1[2], r2[2];
-          const float av[2] = {lo_bf(a[j]), hi_bf(a[j])}, bv[2] = {lo_bf(b[j]), hi_bf(b[j])};
-          const float cv[2] = {lo_bf(cs[j]), hi_bf(cs[j])}, sv[2] = {lo_bf(sn[j]), hi_bf(sn[j])};
+        for (int i0 = 0; i0 < NR; i0 += BATCH) {
+          u32x4 cs[BATCH], sn[BATCH];
 #pragma unroll
-          for (int e = 0; e < 2; ++e) {
-            r1[e] = round_bf(av[e] * cv[e]) - round_bf(bv[e] * sv[e]);
-            r2[e] = round_bf(bv[e] * cv[e]) + round_bf(av[e] * sv[e]);
+          for (int i = 0; i < BATCH; ++i) {
+            const long p = row_pos[tid / (BN / 16) + RSTEP * (i0 + i)];
+            cs[i] = *reinterpret_cast<const u32x4 *>(qe.cos + p * half + j0);
+            sn[i] = *reinterpret_cast<const u32x4 *>(qe.sin + p * half + j0);
           }
-          o1[j] = pack_bf2(r1[0], r1[1]);
-          o2[j] = pack_bf2(r2[0], r2[1]);
+#pragma unroll
+          for (int i = 0; i < BATCH; ++i) {
+            const int row = tid / (BN / 16) + RSTEP * (i0 + i);
+            if (m0 + row >= M) continue;
+            const u32x4 a = *reinterpret_cast<const u32x4 *>(smem + row * OUT_PITCH + c1);
+            const u32x4 b = *reinterpret_cast<const u32x4 *>(smem + row * OUT_PITCH + c1 + half);
+            u32x4 o1, o2;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              float r1[2], r2[2];
+              const float av[2] = {lo_bf(a[j]), hi_bf(a[j])}, bv[2] = {lo_bf(b[j]), hi_bf(b[j])};
+              const float cv[2] = {lo_bf(cs[i][j]), hi_bf(cs[i][j])}, sv[2] = {lo_bf(sn[i][j]), hi_bf(sn[i][j])};
+#pragma unroll
+              for (int e = 0; e < 2; ++e) {
+                r1[e] = round_bf(av[e] * cv[e]) - round_bf(bv[e] * sv[e]);
+                r2[e] = round_bf(bv[e] * cv[e]) + round_bf(av[e] * sv[e]);
+              }
+              o1[j] = pack_bf2(r1[0], r1[1]);
+              o2[j] = pack_bf2(r2[0], r2[1]);
+            }
+            uint16_t *dst = Cb + (long)(m0 + row) * ldc + n0 + c1;
+            *reinterpret_cast<u32x4 *>(dst) = o1;
+            *reinterpret_cast<u32x4 *>(dst + half) = o2;
+          }
         }
-        uint16_t *dst = Cb + (long)(m0 + row) * ldc + n0 + c1;
-        *reinterpret_cast<u32x4 *>(dst) = o1;
-        *reinterpret_cast<u32x4 *>(dst + half) = o2;
       }
       if (vt_tile) {
         // Thread c owns V^T row n0 + c - qk_cols and walks the tile's tokens: 8 tokens whose V^T columns
@@ -548,8 +573,8 @@ gemm_nt_kernel(const uint16_t *__restrict__ A, const uint16_t *__restrict__ B, v
           uint16_t *vrow = qe.vt + (long)(n0 + c - qe.qk_cols) * qe.vt_ld;
           const uint16_t *src = smem + c * TP;
           for (int r = 0; r < valid;) {
-            const int col = qe.vt_col[m0 + r];
-            if ((col & 7) == 0 && r + 8 <= valid && qe.vt_col[m0 + r + 7] == col + 7) {
+            const int col = row_col[r];
+            if ((col & 7) == 0 && r + 8 <= valid && row_col[r + 7] == col + 7) {
               *reinterpret_cast<u32x4 *>(vrow + col) = *reinterpret_cast<const u32x4 *>(src + r);
               r += 8;
             } else {
@@ -563,7 +588,7 @@ gemm_nt_kernel(const uint16_t *__restrict__ A, const uint16_t *__restrict__ B, v
         // n0 + c - qk_cols; the lanes of a store instruction write consecutive V^T columns)
         const int row = tid % BM;
         if (m0 + row < M) {
-          const long col = qe.vt_col[m0 + row];
+          const long col = row_col[row];
           for (int c = max(qe.qk_cols - n0, 0) + tid / BM; c < BN; c += THREADS / BM)
             qe.vt[(long)(n0 + c - qe.qk_cols) * qe.vt_ld + col] = smem[row * OUT_PITCH + c];
         }
@@ -589,7 +614,9 @@ hipError_t launch(const uint16_t *A, const uint16_t *B, void *C, long M, long N,
   // (against the register-staged path: down K 14336 +3-8 % alone and -0.8 % step time in the 9B
   // forward, K 36864 +4.5 %, 1344- and 448-tile down shapes +2.5 % / +1 %). 128-row tiles (M <= 1024)
   // have two stages only, so long K keeps the register-staged path and its two tiles of slack there.
-  auto kern = (BM == 256 || K <= 8192) ? gemm_nt_kernel<BM, EPI, true> : gemm_nt_kernel<BM, EPI, false>;
+  auto kern = gemm_nt_kernel<BM, EPI, true>;
+  if constexpr (BM != 256)
+    if (K > 8192) kern = gemm_nt_kernel<BM, EPI, false>;
   kern<<<dim3((unsigned)(num_m * num_n)), dim3(THREADS), 0, s>>>(A, B, C, (int)M, (int)N, (int)K, lda, ldb, ldc,
                                                                  act, qe);
   return hipGetLastError();
