@@ -215,6 +215,76 @@ def cpu_baseline(cfg, seconds_budget: float = 25.0, n: int = 2048) -> dict:
                       f"{cfg.layers}-layer batch"}
 
 
+PEAK_FP32 = 157.3e12    # MI355X fp32 matrix / vector, FLOP/s
+
+
+def causal_pairs(s: int, window: int = 0) -> int:
+    """Visible (query, key) pairs of one causal sequence of s tokens, window 0 = global."""
+    if window <= 0 or window >= s:
+        return s * (s + 1) // 2
+    return window * (window + 1) // 2 + (s - window) * window
+
+
+def config_kernels(reps: int = 5) -> dict:
+    """The single-kernel configurations beside the forward, timed with HIP events over `reps` calls
+    after one warm-up call (synthetic N(0, 1) inputs scaled as below, random weights):
+    - attention, fp32: batch 1 x 512, 8/4 heads x 128, causal, scale 128^-0.5, no softcap;
+    - attention layer pair, bf16: batch 8 x 2048, 16/8 heads x 256, softcap 50, scale 1/16, the
+      sliding layer (window 4096, inactive at 2048) plus the global layer; and one window-512 layer;
+    - fused MLP, bf16: 8192 rows, H 3584, I 14336, RMSNorm(1 + w) -> GELU-tanh gate|up -> down.
+    Each entry's FLOPs are algorithmic (4 D Hq per visible pair; 6 T H I), the inputs already in HBM."""
+    import torch
+
+    from deciax_amd import kernels as K
+
+    def timed(fn) -> float:
+        fn()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(reps):
+            fn()
+        b.record()
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) / reps
+
+    g = torch.Generator(device="cuda").manual_seed(0)
+    out = {}
+
+    def attn_case(b, s, hq, hkv, d, dtype, scale, softcap, windows):
+        q = torch.randn((b * s, hq * d), generator=g, device="cuda").to(dtype) * 0.5
+        k = torch.randn((b * s, hkv * d), generator=g, device="cuda").to(dtype) * 0.5
+        v = torch.randn((b * s, hkv * d), generator=g, device="cuda").to(dtype) * 0.5
+        starts = torch.arange(b, dtype=torch.int32, device="cuda") * s
+        lens = torch.full((b,), s, dtype=torch.int32, device="cuda")
+        o = torch.empty_like(q)
+        ms = sum(timed(lambda w=w: K.attention_varlen(q, k, v, starts, lens, s, num_q_heads=hq, num_kv_heads=hkv,
+                                                      head_dim=d, scale=scale, softcap=softcap, window=w,
+                                                      out=o)) for w in windows)
+        flops = sum(4.0 * d * hq * b * causal_pairs(s, w) for w in windows)
+        return ms, flops
+
+    ms, fl = attn_case(1, 512, 8, 4, 128, torch.float32, 128 ** -0.5, 0.0, [0])
+    out["attention_fp32_1x512_8/4x128"] = {"ms": round(ms, 4), "tflops": round(fl / ms / 1e9, 2),
+                                           "frac_fp32_peak": round(fl / ms * 1e3 / PEAK_FP32, 4)}
+    ms, fl = attn_case(8, 2048, 16, 8, 256, torch.bfloat16, 1 / 16, 50.0, [4096, 0])
+    out["attention_layer_pair_bf16_8x2048_16/8x256"] = {"ms": round(ms, 3), "tflops": round(fl / ms / 1e9, 2),
+                                                        "frac_bf16_peak": round(fl / ms * 1e3 / PEAK_BF16, 4)}
+    ms, fl = attn_case(8, 2048, 16, 8, 256, torch.bfloat16, 1 / 16, 50.0, [512])
+    out["attention_window512_bf16_8x2048_16/8x256"] = {"ms": round(ms, 3), "tflops": round(fl / ms / 1e9, 2),
+                                                       "frac_bf16_peak": round(fl / ms * 1e3 / PEAK_BF16, 4)}
+    t, h, f = 8192, 3584, 14336
+    x = torch.randn((t, h), generator=g, device="cuda").to(torch.bfloat16)
+    norm = (torch.randn((h,), generator=g, device="cuda") * 0.02).to(torch.bfloat16)
+    gate_up = (torch.randn((2 * f, h), generator=g, device="cuda") * 0.02).to(torch.bfloat16)
+    down = (torch.randn((h, f), generator=g, device="cuda") * 0.02).to(torch.bfloat16)
+    ms = timed(lambda: K.mlp(x, norm, gate_up, down, eps=1e-6))
+    fl = 6.0 * t * h * f
+    out["mlp_bf16_8192x3584x14336"] = {"ms": round(ms, 3), "tflops": round(fl / ms / 1e9, 2),
+                                       "frac_bf16_peak": round(fl / ms * 1e3 / PEAK_BF16, 4)}
+    return out
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -222,6 +292,7 @@ def main() -> None:
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-configs", action="store_true", help="skip the single-kernel configurations")
     ap.add_argument("--model", choices=("gemma2-9b", "gemma2-27b"), default="gemma2-9b")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -292,6 +363,11 @@ def main() -> None:
     attn_ms = sum(kern[k]["total_ms"] for k in kern if k.startswith("attention")) / args.steps
     attn_flops = cfg.attention_flops(lengths)
 
+    configs = None
+    if not args.no_configs:
+        print("# single-kernel configurations", file=sys.stderr, flush=True)
+        configs = config_kernels()
+
     cpu = None
     if not args.no_cpu_baseline:
         print("# cpu baseline (oracle sample)", file=sys.stderr, flush=True)
@@ -327,6 +403,7 @@ def main() -> None:
                       "frac_bf16_peak": round(attn_flops / (attn_ms * 1e-3) / PEAK_BF16, 4),
                       "ms_per_step": round(attn_ms, 2)},
         "kernels": per_kernel,
+        "kernel_configs": configs,
         "roofline": roofline,
         "cpu_baseline": cpu,
     }

@@ -55,6 +55,10 @@ int validate_attn(const void *q, const void *k, const void *v, const void *out, 
   SUPPORTED(d == 64 || d == 128 || d == 256, "attention: head_dim %d not in {64, 128, 256}", d);
   if (dtype == DX_BF16) SUPPORTED(hq / hkv == 1 || hq / hkv == 2 || hq / hkv == 4,
                                   "attention: bf16 GQA group %d not in {1, 2, 4}", hq / hkv);
+  // launch grids: bf16 (query tiles, KV heads, sequences) and its V^T transpose (64-row tiles,
+  // sequences, KV heads x D / 64); fp32 (query tiles, sequences, heads). y and z stop at 65535.
+  SUPPORTED(num_seqs <= 65535 && hq <= 65535, "attention: %d sequences or %d heads beyond the launch grid",
+            num_seqs, hq);
   const int64_t vec = dtype == DX_BF16 ? 8 : 4;
   REQUIRE(qs % vec == 0 && ks % vec == 0 && os % vec == 0, "attention: row strides must be multiples of %ld elements",
           (long)vec);
@@ -149,6 +153,8 @@ int dx_transpose_v(const void *v, void *vt, const int32_t *seq_start, const int3
   SUPPORTED(head_dim % 64 == 0, "transpose_v: head_dim %d not a multiple of 64", head_dim);
   REQUIRE(v_row_stride % 8 == 0 && vt_ld % 8 == 0, "transpose_v: strides must be multiples of 8");
   REQUIRE(num_seqs >= 0 && max_seq_len >= 0 && num_kv_heads > 0, "transpose_v: bad sizes");
+  SUPPORTED(num_seqs <= 65535 && (int64_t)num_kv_heads * (head_dim / 64) <= 65535,
+            "transpose_v: %d sequences or %d heads beyond the launch grid", num_seqs, num_kv_heads);
   if (num_seqs == 0 || max_seq_len == 0) return DX_OK;
   return check_launch(dx_transpose_v_launch(static_cast<const uint16_t *>(v), static_cast<uint16_t *>(vt), seq_start,
                                             seq_len, vt_start, 0, num_seqs, max_seq_len, num_kv_heads, head_dim,

@@ -135,10 +135,16 @@ attn_bf16_kernel(const uint16_t *__restrict__ Q, const uint16_t *__restrict__ K,
   static_assert(WI >= 2 && WI % 2 == 0 && NI % BF_WAVES == 0, "tile too small for the wave count");
   __shared__ __attribute__((aligned(1024))) uint16_t smem[NSTAGE * STAGE];
 
-  const int b = blockIdx.y, g = blockIdx.z;
+  // Grid (query tile, KV head, sequence), the tile index counted from the last: within each (sequence,
+  // head) the heaviest tiles launch first, and consecutive workgroups stream the same K and V^T tiles
+  // nearly in step, so most of their reads hit in L2. Sequences launch in the order of the descriptor
+  // arrays; the forward driver lists the longest first. (Launching the heaviest tiles of all sequences
+  // first instead balances a batch of equal lengths better, +33% at 8 x 2048, but scatters the
+  // concurrent K and V^T streams: -30% on a batch of ragged lengths up to 16K.)
+  const int g = blockIdx.y, b = blockIdx.z;
   const int len = min(max(seq_len[b], 0), max_seq_len);
   const int ntiles = (max_seq_len + BQ - 1) / BQ;
-  const int q0 = (ntiles - 1 - (int)blockIdx.x) * BQ;  // latest (heaviest) tiles launch first
+  const int q0 = (ntiles - 1 - (int)blockIdx.x) * BQ;
   if (q0 >= len) return;
   const long start = seq_start[b];
   const long vts = vt_start ? (long)vt_start[b] : (long)b * vt_seq_stride;
@@ -528,7 +534,7 @@ vt_zero_tails_kernel(uint16_t *__restrict__ Vt, const int32_t *__restrict__ seq_
 template <int D, int G>
 hipError_t launch_bf16_dg(const AttnArgs &a, hipStream_t s) {
   constexpr int BQ = 32 * (BF_WAVES / G);
-  const dim3 grid((a.max_seq_len + BQ - 1) / BQ, a.num_seqs, a.hkv);
+  const dim3 grid((a.max_seq_len + BQ - 1) / BQ, a.hkv, a.num_seqs);
   const bool fixed = a.softcap > 0.f && a.softcap <= 56.f;
   auto kern = fixed ? attn_bf16_kernel<D, G, MODE_FIXED> : attn_bf16_kernel<D, G, MODE_ONLINE>;
   kern<<<grid, dim3(BF_THREADS), 0, s>>>(

@@ -291,6 +291,9 @@ class PackedBatch:
     q_offsets: torch.Tensor
     questions_per_request: list[int] = field(default_factory=list)
     options_per_question: list[int] = field(default_factory=list)
+    # (seq_start, seq_len, vt_start) listed longest request first: the attention kernel launches
+    # sequences in descriptor order, so the heaviest work starts first (outputs do not depend on it)
+    by_length: tuple[torch.Tensor, torch.Tensor, torch.Tensor] | None = None
 
     @property
     def rows(self) -> int:
@@ -329,8 +332,11 @@ def pack_batch(token_ids: Sequence[Sequence[int]], options: Sequence[Sequence[Se
         return torch.as_tensor(np.asarray(a, dtype=np.int64).astype(np.int32)).to(dev)
 
     vt_col = np.repeat(vt_start, lengths) + positions
+    order = np.argsort(-np.asarray(lengths), kind="stable")
+    by_length = (i32(starts[order]), i32(np.asarray(lengths)[order]), i32(vt_start[order]))
     return PackedBatch(lengths, i32(ids), i32(positions), i32(starts), i32(lengths), i32(vt_start),
-                       int(sum(padded)), i32(vt_col), i32(opt_pos), i32(opt_label), i32(q_off), qpr, opq)
+                       int(sum(padded)), i32(vt_col), i32(opt_pos), i32(opt_label), i32(q_off), qpr, opq,
+                       by_length)
 
 
 class Workspace:
@@ -367,10 +373,10 @@ def layer_forward(w: DecisionWeights, i: int, batch: PackedBatch, ws: Workspace)
     vt = ws.vt[:, :batch.vt_ld]
     K.qkv_rope(h, lw.qkv, qkv, vt, batch.positions, batch.vt_col, w.cos, w.sin, num_q_heads=c.heads,
                num_kv_heads=c.kv_heads, head_dim=c.head_dim)
-    K.attention_vt(qkv[:, :qd], qkv[:, qd:qd + kd], vt, batch.seq_start, batch.seq_len, batch.vt_start,
-                   batch.max_len, num_q_heads=c.heads, num_kv_heads=c.kv_heads, head_dim=c.head_dim,
-                   scale=c.query_scale, softcap=c.attn_softcap, window=c.window if c.sliding(i) else 0,
-                   causal=True, out=att)
+    seq_start, seq_len, vt_start = batch.by_length or (batch.seq_start, batch.seq_len, batch.vt_start)
+    K.attention_vt(qkv[:, :qd], qkv[:, qd:qd + kd], vt, seq_start, seq_len, vt_start, batch.max_len,
+                   num_q_heads=c.heads, num_kv_heads=c.kv_heads, head_dim=c.head_dim, scale=c.query_scale,
+                   softcap=c.attn_softcap, window=c.window if c.sliding(i) else 0, causal=True, out=att)
     K.linear(att, lw.o, out=y)
     K.add_rmsnorm(y, x, eps=c.eps, post_w=lw.post_attn_norm, next_w=lw.pre_ffn_norm, h=h)
     K.gated_linear(h, lw.gate_up, c.activation, out=act)

@@ -94,7 +94,9 @@ int64_t dx_attn_prefill_workspace(int32_t num_seqs, int32_t max_seq_len,
  * vt_start[s] + p]. This is the layout dx_transpose_v writes; the model
  * driver produces it once per layer. Each vt_start[s] is a multiple of 8 and
  * columns [vt_start[s], vt_start[s] + seq_len[s] rounded up to 64) lie inside
- * vt_ld and hold zeros past seq_len[s] (dx_transpose_v writes them). */
+ * vt_ld and hold zeros past seq_len[s] (dx_transpose_v writes them). The
+ * sequences may be listed in any order and are launched in that order;
+ * listing the longest first starts the heaviest work first. */
 int dx_attn_prefill_vt(const void *q, const void *k, const void *vt, void *out,
                        const int32_t *seq_start, const int32_t *seq_len,
                        const int32_t *vt_start, int32_t num_seqs,

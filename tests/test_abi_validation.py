@@ -70,3 +70,19 @@ def test_every_entry_point_has_a_signature_bound(name: str) -> None:
     fn = getattr(lib(), name)
     restype, argtypes = _lib.SIGNATURES[name]
     assert fn.restype == restype and list(fn.argtypes) == list(argtypes)
+
+
+
+def test_attention_grid_limits() -> None:
+    """Counts beyond what a launch grid's y / z dimension holds are refused, not launched."""
+    f = ctypes.c_float
+
+    def vt(nseq, maxlen, hq=4, hkv=2):
+        return status("dx_attn_prefill_vt", P, P, P, P, P, P, P, nseq, maxlen, hq, hkv, 128, 512, 256, 4096, 512,
+                      f(0.1), f(50.0), 0, 1, NUL)
+
+    for got in (vt(70000, 64), vt(4, 64, hq=140000, hkv=70000)):
+        assert got == _lib.DX_ERR_UNSUPPORTED
+        assert b"launch grid" in lib().dx_last_error()
+    check("dx_transpose_v", _lib.DX_ERR_UNSUPPORTED, P, P, P, P, P, 70000, 64, 2, 128, 256, 4096, NUL)
+    check("dx_transpose_v", _lib.DX_OK, P, P, P, P, P, 0, 64, 2, 128, 256, 4096, NUL)

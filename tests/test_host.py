@@ -328,3 +328,32 @@ def test_bench_refuses_several_gpus() -> None:
                          timeout=120, cwd=root)
     assert res.returncode == 2
     assert "--gpus 1" in res.stderr and res.stdout == ""
+
+
+def test_bench_causal_pairs() -> None:
+    """The visible-pair count behind the single-kernel configurations' FLOPs: brute force on small
+    sequences, and the attention-layer figures the benchmark reports at 8 x 2048."""
+    import bench
+
+    for s in (1, 2, 7, 64, 65):
+        for w in (0, 1, 3, 64, 100):
+            want = sum(1 for i in range(s) for j in range(i + 1) if w <= 0 or i - j < w)
+            assert bench.causal_pairs(s, w) == want, (s, w)
+    assert bench.causal_pairs(2048) == 2_098_176
+    assert bench.causal_pairs(2048, 4096) == 2_098_176
+    assert bench.causal_pairs(2048, 512) == 917_760
+    assert 4 * 256 * 16 * 8 * bench.causal_pairs(2048) == 275_012_124_672  # 2.750e11 FLOP per layer
+
+
+def test_pack_batch_longest_first_descriptors() -> None:
+    """The attention kernel launches sequences in descriptor order; the driver hands it the packed
+    batch's (seq_start, seq_len, vt_start) listed longest first (stable among equal lengths), each
+    triple unchanged."""
+    from deciax_amd.gemma import pack_batch
+
+    b = pack_batch([[1] * 5, [2] * 70, [3] * 70, [4] * 1], [[], [], [], []], device="cpu")
+    ss, sl, vs = b.by_length
+    order = [1, 2, 0, 3]
+    assert sl.tolist() == [70, 70, 5, 1]
+    assert ss.tolist() == [b.seq_start.tolist()[i] for i in order]
+    assert vs.tolist() == [b.vt_start.tolist()[i] for i in order]
