@@ -39,6 +39,7 @@ constexpr int BF_WAVES = 8;         // bf16 path: two waves per SIMD
 constexpr int BF_THREADS = 64 * BF_WAVES;
 constexpr int BKV = 64;     // V^T block alignment of dx_transpose_v
 constexpr int NSTAGE = 4;   // LDS ring depth of the bf16 path
+constexpr int SHORT_SEQ = 4096;  // bf16 grid order switch (see attn_bf16_kernel)
 constexpr float LOG2E = 1.4426950408889634f;
 constexpr float NEG_BIG = -1e30f;  // the reference's MASK_FILL (reference.py:8)
 
@@ -135,16 +136,20 @@ attn_bf16_kernel(const uint16_t *__restrict__ Q, const uint16_t *__restrict__ K,
   static_assert(WI >= 2 && WI % 2 == 0 && NI % BF_WAVES == 0, "tile too small for the wave count");
   __shared__ __attribute__((aligned(1024))) uint16_t smem[NSTAGE * STAGE];
 
-  // Grid (query tile, KV head, sequence), the tile index counted from the last: within each (sequence,
-  // head) the heaviest tiles launch first, and consecutive workgroups stream the same K and V^T tiles
-  // nearly in step, so most of their reads hit in L2. Sequences launch in the order of the descriptor
-  // arrays; the forward driver lists the longest first. (Launching the heaviest tiles of all sequences
-  // first instead balances a batch of equal lengths better, +33% at 8 x 2048, but scatters the
-  // concurrent K and V^T streams: -30% on a batch of ragged lengths up to 16K.)
-  const int g = blockIdx.y, b = blockIdx.z;
+  // Grid order, the query tile index counted from the last (heaviest first):
+  // - max_seq_len > SHORT_SEQ: (query tile, KV head, sequence). Consecutive workgroups stream one
+  //   (sequence, head)'s K and V^T tiles nearly in step, so most reads hit in L2; sequences launch in
+  //   descriptor order, and the forward driver lists the longest first.
+  // - otherwise: (KV head, sequence, query tile), the heaviest tiles of every sequence first. With short
+  //   sequences a single tile is a large share of a CU's work, so the order above leaves a tail
+  //   (8 x 2048: +33% this way), while each (sequence, head)'s K and V^T (<= 4 MB) fit in an XCD's L2.
+  //   On ragged lengths up to 16K this order costs 25-35% instead: the concurrent streams scatter.
+  const bool tile_major = max_seq_len <= SHORT_SEQ;
+  const int g = tile_major ? blockIdx.x : blockIdx.y, b = tile_major ? blockIdx.y : blockIdx.z;
+  const int qt = tile_major ? blockIdx.z : blockIdx.x;
   const int len = min(max(seq_len[b], 0), max_seq_len);
   const int ntiles = (max_seq_len + BQ - 1) / BQ;
-  const int q0 = (ntiles - 1 - (int)blockIdx.x) * BQ;
+  const int q0 = (ntiles - 1 - qt) * BQ;
   if (q0 >= len) return;
   const long start = seq_start[b];
   const long vts = vt_start ? (long)vt_start[b] : (long)b * vt_seq_stride;
@@ -534,7 +539,8 @@ vt_zero_tails_kernel(uint16_t *__restrict__ Vt, const int32_t *__restrict__ seq_
 template <int D, int G>
 hipError_t launch_bf16_dg(const AttnArgs &a, hipStream_t s) {
   constexpr int BQ = 32 * (BF_WAVES / G);
-  const dim3 grid((a.max_seq_len + BQ - 1) / BQ, a.hkv, a.num_seqs);
+  const unsigned ntiles = (a.max_seq_len + BQ - 1) / BQ;
+  const dim3 grid = a.max_seq_len <= SHORT_SEQ ? dim3(a.hkv, a.num_seqs, ntiles) : dim3(ntiles, a.hkv, a.num_seqs);
   const bool fixed = a.softcap > 0.f && a.softcap <= 56.f;
   auto kern = fixed ? attn_bf16_kernel<D, G, MODE_FIXED> : attn_bf16_kernel<D, G, MODE_ONLINE>;
   kern<<<grid, dim3(BF_THREADS), 0, s>>>(
