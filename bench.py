@@ -148,6 +148,15 @@ def algorithmic_work(cfg, lengths: list[int]) -> dict[str, float]:
     }
 
 
+def algorithmic_bytes(cfg, lengths: list[int]) -> dict[str, float]:
+    """Algorithmic HBM bytes of one average launch of the memory-bound kernels: add_rmsnorm reads y and
+    the residual x and writes x and the next block's normed h, bf16 [T, H] each; the last of the 2 L
+    launches has no next norm and writes no h."""
+    th = 2.0 * sum(lengths) * cfg.hidden
+    launches = 2 * cfg.layers
+    return {"add_rmsnorm": ((launches - 1) * 4 * th + 3 * th) / launches}
+
+
 TRAFFIC_PROFILES = {("gemma2-9b", "gate_up_proj"): ROOT / "profiles" / "gate_up_gemm_traffic.md"}
 
 
@@ -339,6 +348,7 @@ def main() -> None:
 
     kern = timer.summary()
     work = algorithmic_work(cfg, lengths)
+    nbytes = algorithmic_bytes(cfg, lengths)
     total_flops = tokens * cfg.linear_flops_per_token() + cfg.attention_flops(lengths)
     per_kernel = {}
     for name, s in sorted(kern.items(), key=lambda kv: -kv[1]["total_ms"]):
@@ -347,6 +357,9 @@ def main() -> None:
         if name in work and s["launches"]:
             entry["tflops"] = work[name] / (s["avg_ms"] * 1e-3) / 1e12
             entry["frac_bf16_peak"] = entry["tflops"] * 1e12 / PEAK_BF16
+        if name in nbytes and s["launches"]:
+            entry["gbps"] = nbytes[name] / (s["avg_ms"] * 1e-3) / 1e9
+            entry["frac_hbm_peak"] = entry["gbps"] * 1e9 / PEAK_HBM
         per_kernel[name] = entry
     dominant = max(kern, key=lambda k: kern[k]["total_ms"])
     dom = per_kernel[dominant]

@@ -357,3 +357,14 @@ def test_pack_batch_longest_first_descriptors() -> None:
     assert sl.tolist() == [70, 70, 5, 1]
     assert ss.tolist() == [b.seq_start.tolist()[i] for i in order]
     assert vs.tolist() == [b.vt_start.tolist()[i] for i in order]
+
+
+def test_bench_norm_bytes() -> None:
+    """add_rmsnorm's algorithmic bytes: 4 bf16 [T, H] tensors per launch, 3 in the last of 2 L."""
+    import bench
+    from deciax_amd.gemma import CONFIGS
+
+    cfg = CONFIGS["gemma2-9b"]
+    t = 70471
+    per = bench.algorithmic_bytes(cfg, [t])["add_rmsnorm"]
+    assert per * 84 == 83 * 4 * 2 * t * 3584 + 3 * 2 * t * 3584
