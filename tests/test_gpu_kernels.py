@@ -216,6 +216,44 @@ def test_attention_vt_path_matches_generic() -> None:
         assert (vt_np[:, p0 + n:p0 + (n + 63) // 64 * 64] == 0).all()
 
 
+@pytest.mark.parametrize("hq,hkv,d", [(16, 8, 256), (32, 16, 128)])
+@pytest.mark.parametrize("window", [4096, 0])
+def test_attention_long_sequences_and_descriptor_order(hq: int, hkv: int, d: int, window: int) -> None:
+    """Batches with a sequence longer than 4096 tokens take the (query tile, KV head, sequence) grid:
+    sampled rows of a 5000-token sequence (window 4096 active), a 4097- and a 300-token one against
+    the oracle; and the output is bit-identical when the sequence descriptors are listed longest
+    first, the order the forward driver uses."""
+    import torch
+
+    from deciax_amd import kernels as K
+    from oracle.attention import attention_seq
+
+    say(f"attention long sequences hq={hq} hkv={hkv} d={d} window={window}")
+    lengths = [300, 5000, 4097]
+    q, k, v, starts = _packed_case(5 + d + window, lengths, hq, hkv, d)
+    rows = q.shape[0]
+    qd, kd, vd = (to_dev(a.reshape(rows, -1)) for a in (q, k, v))
+    padded = [(n + 63) // 64 * 64 for n in lengths]
+    vt_start = np.concatenate([[0], np.cumsum(padded)[:-1]])
+    vt = torch.zeros((hkv * d, int(sum(padded))), dtype=torch.bfloat16, device="cuda")
+    K.transpose_v(vd, vt, i32(starts), i32(lengths), i32(vt_start), max(lengths), num_kv_heads=hkv, head_dim=d)
+
+    def run(order: list[int]) -> np.ndarray:
+        return to_np(K.attention_vt(qd, kd, vt, i32(starts[order]), i32(np.asarray(lengths)[order]),
+                                    i32(vt_start[order]), max(lengths), num_q_heads=hq, num_kv_heads=hkv,
+                                    head_dim=d, scale=d ** -0.5, softcap=50.0, window=window))
+
+    got = run([0, 1, 2])
+    np.testing.assert_array_equal(got, run([1, 2, 0]))
+    got = got.reshape(rows, hq, d)
+    r = rng(3)
+    for s, n in zip(starts, lengths):
+        qpos = np.unique(np.concatenate([[0, n // 2, n - 1], r.choice(n, 6, replace=False)]))
+        want = attention_seq(q[s:s + n], k[s:s + n], v[s:s + n], scale=d ** -0.5, softcap_value=50.0, window=window,
+                             query_pos=qpos)
+        close(got[s + qpos], want, 2e-2)
+
+
 def test_attention_fp32_config1() -> None:
     """Single causal GQA prefill in fp32: B1 S512 8/4 heads x 128, q/k/v ~ N(0,1) from seed 0, 1e-4."""
     from deciax_amd import kernels as K
