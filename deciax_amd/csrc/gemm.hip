@@ -616,9 +616,11 @@ hipError_t launch(const uint16_t *A, const uint16_t *B, void *C, long M, long N,
   auto kern = gemm_nt_kernel<BM, EPI, true>;
   if constexpr (BM != 256)
     if (K > 8192) kern = gemm_nt_kernel<BM, EPI, false>;
-  // Tile rows walked together per XCD: 8, or 2 for long K, where an A row tile is megabytes and the
-  // groups of 8 re-read it once per 4 column tiles (9B down, K 14336: +3%; K 36864 and short K: 0%).
-  const int group_m = K >= 8192 ? 2 : 8;
+  // Tile rows walked together per XCD: 2 for long K, where an A row tile is megabytes and groups of 8
+  // re-read it once per 4 column tiles (9B down, K 14336: +4%; K 36864: 0%); 4 for the plain bf16 /
+  // fp32 epilogues (o at 9B and 27B: +1.5-2%); 8 for the gated and q|k|v epilogues, where 4 measured
+  // mixed (27B q|k|v -4.7%).
+  const int group_m = K >= 8192 ? 2 : (EPI == EPI_BF16 || EPI == EPI_F32) ? 4 : 8;
   kern<<<dim3((unsigned)(num_m * num_n)), dim3(THREADS), 0, s>>>(A, B, C, (int)M, (int)N, (int)K, lda, ldb, ldc,
                                                                  act, group_m, qe);
   return hipGetLastError();
