@@ -310,9 +310,15 @@ def attention_vt(q: torch.Tensor, k: torch.Tensor, vt: torch.Tensor, seq_start: 
                  vt_start: torch.Tensor, max_seq_len: int, *, num_q_heads: int, num_kv_heads: int, head_dim: int,
                  scale: float, softcap: float = 0.0, window: int = 0, causal: bool = True,
                  out: torch.Tensor | None = None) -> torch.Tensor:
-    """bf16 attention with V pre-transposed by `transpose_v` (the model driver's form)."""
+    """bf16 attention with V pre-transposed by `transpose_v` (the model driver's form). The sequence
+    descriptors (int32 seq_start, seq_len, vt_start) may come in any order; the kernel launches them
+    in that order, so listing the longest first starts the heaviest work first."""
     for t, n in ((q, "q"), (k, "k"), (vt, "vt")):
         _need(t, n, BF16, 2)
+    for t, n in ((seq_start, "seq_start"), (seq_len, "seq_len"), (vt_start, "vt_start")):
+        _need(t, n, torch.int32, 1)
+    if not seq_start.shape[0] == seq_len.shape[0] == vt_start.shape[0]:
+        raise ValueError("attention_vt: seq_start, seq_len and vt_start need one entry per sequence")
     if out is None:
         out = torch.empty((q.shape[0], num_q_heads * head_dim), dtype=BF16, device=q.device)
     call("dx_attn_prefill_vt", _ptr(q), _ptr(k), _ptr(vt), _ptr(out), _ptr(seq_start), _ptr(seq_len),

@@ -526,3 +526,11 @@ def test_abi_rejects_bad_arguments() -> None:
     with pytest.raises(ValueError, match="GQA group"):
         K.attention_varlen(q, q[:, :64], q[:, :64], i32([0]), i32([8]), 8, num_q_heads=8, num_kv_heads=1,
                            head_dim=64, scale=1.0)
+    vt = torch.zeros((64, 64), dtype=torch.bfloat16, device="cuda")
+    starts64 = torch.zeros(1, dtype=torch.int64, device="cuda")
+    with pytest.raises(ValueError, match="seq_start must be torch.int32"):
+        K.attention_vt(q, q[:, :64], vt, starts64, i32([8]), i32([0]), 8, num_q_heads=8, num_kv_heads=1, head_dim=64,
+                       scale=1.0)
+    with pytest.raises(ValueError, match="one entry per sequence"):
+        K.attention_vt(q, q[:, :64], vt, i32([0, 8]), i32([8]), i32([0]), 8, num_q_heads=8, num_kv_heads=1,
+                       head_dim=64, scale=1.0)
