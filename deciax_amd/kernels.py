@@ -211,8 +211,17 @@ def add_rmsnorm(y: torch.Tensor, x: torch.Tensor, *, eps: float, post_w: torch.T
     if y.shape != x.shape or not (x.is_contiguous() and y.is_contiguous()):
         raise ValueError("add_rmsnorm: y and x must be contiguous and of one shape")
     rows, d = x.shape
+    for t, n in ((post_w, "post_w"), (next_w, "next_w")):
+        if t is not None:
+            _need(t, n, BF16, 1)
+            if t.shape[0] != d or not t.is_contiguous():
+                raise ValueError(f"add_rmsnorm: {n} must be a contiguous [{d}] tensor")
     if next_w is not None and h is None:
         h = torch.empty_like(x)
+    if next_w is not None:
+        _need(h, "h", BF16, 2)
+        if h.shape != x.shape or not h.is_contiguous():
+            raise ValueError("add_rmsnorm: h must be contiguous and of x's shape")
     call("dx_add_rmsnorm", _ptr(y), _ptr(post_w), _ptr(x), _ptr(next_w), _ptr(h if next_w is not None else None),
          rows, d, float(eps), _stream())
     return h if next_w is not None else None
@@ -231,8 +240,14 @@ def embed(ids: torch.Tensor, table: torch.Tensor, *, scale: float = 1.0, norm_w:
     if norm_w is not None and h is None:
         h = torch.empty_like(x)
     for t, n in ((x, "x"), (h, "h")):
-        if t is not None and (tuple(t.shape) != (ids.shape[0], d) or not t.is_contiguous()):
-            raise ValueError(f"embed: {n} must be a contiguous [tokens, d] tensor")
+        if t is not None:
+            _need(t, n, BF16, 2)
+            if tuple(t.shape) != (ids.shape[0], d) or not t.is_contiguous():
+                raise ValueError(f"embed: {n} must be a contiguous [tokens, d] tensor")
+    if norm_w is not None:
+        _need(norm_w, "norm_w", BF16, 1)
+        if norm_w.shape[0] != d or not norm_w.is_contiguous():
+            raise ValueError(f"embed: norm_w must be a contiguous [{d}] tensor")
     h = h if norm_w is not None else None
     call("dx_embed", _ptr(ids.contiguous()), _ptr(table), _ptr(x), ids.shape[0], d, vocab, float(scale),
          _ptr(norm_w), _ptr(h), float(eps), _stream())
@@ -289,6 +304,10 @@ def transpose_v(v: torch.Tensor, vt: torch.Tensor, seq_start: torch.Tensor, seq_
                 vt_start: torch.Tensor, max_seq_len: int, *, num_kv_heads: int, head_dim: int) -> torch.Tensor:
     _need(v, "v", BF16, 2)
     _need(vt, "vt", BF16, 2)
+    for t, n in ((seq_start, "seq_start"), (seq_len, "seq_len"), (vt_start, "vt_start")):
+        _need(t, n, torch.int32, 1)
+    if not seq_start.shape[0] == seq_len.shape[0] == vt_start.shape[0]:
+        raise ValueError("transpose_v: seq_start, seq_len and vt_start need one entry per sequence")
     call("dx_transpose_v", _ptr(v), _ptr(vt), _ptr(seq_start), _ptr(seq_len), _ptr(vt_start), seq_start.shape[0],
          max_seq_len, num_kv_heads, head_dim, _rows(v, "v"), _rows(vt, "vt"), _stream())
     return vt
@@ -464,6 +483,10 @@ def gather_rows_f32(x: torch.Tensor, index: torch.Tensor, *, batch: int, out: to
 def head_routing_f32(options: torch.Tensor, base: torch.Tensor, option_field: torch.Tensor,
                      option_mask: torch.Tensor, *, batch: int) -> torch.Tensor:
     """Per-field softmax over the owned options and the routed summary (head.py:77-85)."""
+    _f32(options, "options")
+    _f32(base, "base")
+    _need(option_field, "option_field", torch.int32)
+    _need(option_mask, "option_mask", torch.uint8)
     out = torch.empty_like(base)
     call("dx_head_routing_f32", _ptr(options), _ptr(base), _ptr(option_field), _ptr(option_mask), _ptr(out), batch,
          options.shape[0] // batch, base.shape[0] // batch, base.shape[1], _stream())
@@ -472,6 +495,10 @@ def head_routing_f32(options: torch.Tensor, base: torch.Tensor, option_field: to
 
 def head_fields_init_f32(base: torch.Tensor, summary_norm: torch.Tensor, global_proj: torch.Tensor,
                          type_embedding: torch.Tensor, types: torch.Tensor, *, batch: int) -> torch.Tensor:
+    for t, n in ((base, "base"), (summary_norm, "summary_norm"), (global_proj, "global_proj"),
+                 (type_embedding, "type_embedding")):
+        _f32(t, n)
+    _need(types, "types", torch.int32)
     out = torch.empty_like(base)
     call("dx_head_fields_init_f32", _ptr(base), _ptr(summary_norm), _ptr(global_proj), _ptr(type_embedding),
          _ptr(types), _ptr(out), batch, base.shape[0] // batch, base.shape[1], type_embedding.shape[0], _stream())
@@ -481,6 +508,10 @@ def head_fields_init_f32(base: torch.Tensor, summary_norm: torch.Tensor, global_
 def head_features_f32(fields: torch.Tensor, options: torch.Tensor, questions: torch.Tensor,
                       global_vector: torch.Tensor, lexical: torch.Tensor, option_field: torch.Tensor, *, batch: int,
                       prior_scale: float) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    for t, nm in ((fields, "fields"), (options, "options"), (questions, "questions"), (global_vector, "global_vector"),
+                  (lexical, "lexical")):
+        _f32(t, nm)
+    _need(option_field, "option_field", torch.int32)
     n, width = fields.shape
     features = torch.empty((n, 4 * width), dtype=F32, device=fields.device)
     prior = torch.empty(n, dtype=F32, device=fields.device)
@@ -493,6 +524,11 @@ def head_features_f32(fields: torch.Tensor, options: torch.Tensor, questions: to
 
 def head_combine_f32(prior: torch.Tensor, cosine: torch.Tensor, residual: torch.Tensor, option_mask: torch.Tensor, *,
                      gate: float, joint_scale: float) -> torch.Tensor:
+    for t, n in ((prior, "prior"), (cosine, "cosine"), (residual, "residual")):
+        _need(t, n, F32, 1)
+    _need(option_mask, "option_mask", torch.uint8, 1)
+    if not prior.numel() == cosine.numel() == residual.numel() == option_mask.numel():
+        raise ValueError("head_combine_f32: one prior, cosine, residual and mask entry per option")
     out = torch.empty_like(prior)
     call("dx_head_combine_f32", _ptr(prior), _ptr(cosine), _ptr(residual), _ptr(option_mask), _ptr(out),
          prior.numel(), float(gate), float(joint_scale), _stream())

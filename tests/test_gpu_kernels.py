@@ -534,3 +534,11 @@ def test_abi_rejects_bad_arguments() -> None:
     with pytest.raises(ValueError, match="one entry per sequence"):
         K.attention_vt(q, q[:, :64], vt, i32([0, 8]), i32([8]), i32([0]), 8, num_q_heads=8, num_kv_heads=1,
                        head_dim=64, scale=1.0)
+    xr = torch.zeros((4, 512), dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(ValueError, match="post_w must be a contiguous"):
+        K.add_rmsnorm(xr.clone(), xr, eps=1e-6, post_w=torch.zeros(256, dtype=torch.bfloat16, device="cuda"))
+    with pytest.raises(ValueError, match="h must be contiguous"):
+        K.add_rmsnorm(xr.clone(), xr, eps=1e-6, next_w=torch.zeros(512, dtype=torch.bfloat16, device="cuda"),
+                      h=torch.zeros((4, 256), dtype=torch.bfloat16, device="cuda"))
+    with pytest.raises(ValueError, match="norm_w must be a contiguous"):
+        K.embed(i32([0, 1]), xr, norm_w=torch.zeros(256, dtype=torch.bfloat16, device="cuda"))
