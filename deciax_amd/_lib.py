@@ -38,6 +38,12 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
          c_float, c_float, c_int32, c_int32, c_int32, _p, c_int64, _p],
     ),
     "dx_attn_prefill_workspace": (c_int64, [c_int32, c_int32, c_int32, c_int32, c_int32]),
+    "dx_attn_prefill_masked": (
+        c_int,
+        [_p, _p, _p, _p, _p, _p, _p, c_int32, c_int32, c_int32, c_int32, c_int32, c_int64, c_int64, c_int64,
+         c_int64, c_float, c_float, c_int32, c_int32, c_int32, _p, c_int64, _p],
+    ),
+    "dx_attn_prefill_masked_workspace": (c_int64, [c_int32, c_int32, c_int32, c_int32, c_int32]),
     "dx_attn_prefill_vt": (
         c_int,
         [_p, _p, _p, _p, _p, _p, _p, c_int32, c_int32, c_int32, c_int32, c_int32, c_int64, c_int64, c_int64, c_int64,

@@ -41,6 +41,10 @@ hipStream_t as_stream(void *s) { return reinterpret_cast<hipStream_t>(s); }
 
 int64_t align_up(int64_t v, int64_t a) { return (v + a - 1) / a * a; }
 
+// Key-mask words per sequence: whole 64-key tiles, since a tile's second 32-key block may start past the
+// sequence's last key.
+int32_t key_mask_words(int64_t max_seq_len) { return (int32_t)(align_up(max_seq_len, 64) / 32); }
+
 int validate_attn(const void *q, const void *k, const void *v, const void *out, const int32_t *seq_start,
                   const int32_t *seq_len, int32_t num_seqs, int32_t max_seq_len, int32_t hq, int32_t hkv,
                   int32_t d, int64_t qs, int64_t ks, int64_t os, float scale, float softcap, int32_t window,
@@ -65,6 +69,20 @@ int validate_attn(const void *q, const void *k, const void *v, const void *out, 
   REQUIRE(qs >= (int64_t)hq * d && ks >= (int64_t)hkv * d && os >= (int64_t)hq * d,
           "attention: row stride smaller than heads * head_dim");
   REQUIRE(aligned16(q) && aligned16(k) && aligned16(v) && aligned16(out), "attention: pointers must be 16-byte aligned");
+  return DX_OK;
+}
+
+// The bf16 kernel reads one sequence's K rows and one KV head's V^T block through buffer resources whose
+// byte ranges and per-lane offsets are 32-bit: len * k_stride * 2 bytes of K, and
+// ((D - 1) * vt_ld + len rounded up to 64) * 2 bytes of V^T. Larger spans would wrap.
+int check_bf16_ranges(int64_t max_seq_len, int64_t k_stride, int64_t d, int64_t vt_ld) {
+  const int64_t lim = INT64_C(1) << 31;
+  SUPPORTED(max_seq_len * k_stride * 2 < lim,
+            "attention: %ld keys x k row stride %ld exceed the kernel's 2 GiB K range", (long)max_seq_len,
+            (long)k_stride);
+  SUPPORTED(((d - 1) * vt_ld + align_up(max_seq_len, 64)) * 2 < lim,
+            "attention: V^T leading dimension %ld x head_dim %ld exceeds the kernel's 2 GiB V^T range", (long)vt_ld,
+            (long)d);
   return DX_OK;
 }
 
@@ -97,11 +115,24 @@ int64_t dx_attn_prefill_workspace(int32_t num_seqs, int32_t max_seq_len, int32_t
   return align_up(max_seq_len, 64) * num_seqs * num_kv_heads * head_dim * 2;
 }
 
-int dx_attn_prefill(const void *q, const void *k, const void *v, void *out, const int32_t *seq_start,
-                    const int32_t *seq_len, int32_t num_seqs, int32_t max_seq_len, int32_t num_q_heads,
-                    int32_t num_kv_heads, int32_t head_dim, int64_t q_row_stride, int64_t k_row_stride,
-                    int64_t v_row_stride, int64_t out_row_stride, float scale, float softcap, int32_t window,
-                    int32_t causal, int32_t dtype, void *workspace, int64_t workspace_bytes, void *stream) {
+int64_t dx_attn_prefill_masked_workspace(int32_t num_seqs, int32_t max_seq_len, int32_t num_kv_heads,
+                                         int32_t head_dim, int32_t dtype) {
+  if (dtype != DX_BF16 || num_seqs <= 0 || max_seq_len <= 0) return 0;
+  // V^T, then the key mask as bits: two 32-bit words per 64 keys (whole key tiles) per sequence.
+  return align_up(dx_attn_prefill_workspace(num_seqs, max_seq_len, num_kv_heads, head_dim, dtype), 256) +
+         (int64_t)num_seqs * key_mask_words(max_seq_len) * 4;
+}
+
+}  // extern "C"
+
+namespace {
+
+int attn_prefill(const void *q, const void *k, const void *v, const uint8_t *key_mask, void *out,
+                 const int32_t *seq_start, const int32_t *seq_len, int32_t num_seqs, int32_t max_seq_len,
+                 int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim, int64_t q_row_stride,
+                 int64_t k_row_stride, int64_t v_row_stride, int64_t out_row_stride, float scale, float softcap,
+                 int32_t window, int32_t causal, int32_t dtype, void *workspace, int64_t workspace_bytes,
+                 void *stream) {
   int st = validate_attn(q, k, v, out, seq_start, seq_len, num_seqs, max_seq_len, num_q_heads, num_kv_heads,
                          head_dim, q_row_stride, k_row_stride, out_row_stride, scale, softcap, window, dtype);
   if (st) return st;
@@ -111,11 +142,17 @@ int dx_attn_prefill(const void *q, const void *k, const void *v, void *out, cons
   if (num_seqs == 0 || max_seq_len == 0) return DX_OK;
   AttnArgs a{q, k, v, out, seq_start, seq_len, nullptr, num_seqs, max_seq_len, num_q_heads, num_kv_heads, head_dim,
              q_row_stride, k_row_stride, v_row_stride, out_row_stride, 0, scale, softcap, window, causal ? 1 : 0};
+  a.key_mask = key_mask;
   if (dtype == DX_F32) return check_launch(dx_attn_f32(a, as_stream(stream)), "attention fp32 launch");
 
   const int64_t seq_stride = align_up(max_seq_len, 64);
   const int64_t vt_ld = seq_stride * num_seqs;
-  const int64_t need = dx_attn_prefill_workspace(num_seqs, max_seq_len, num_kv_heads, head_dim, DX_BF16);
+  st = check_bf16_ranges(max_seq_len, k_row_stride, head_dim, vt_ld);
+  if (st) return st;
+  const int64_t vt_bytes = dx_attn_prefill_workspace(num_seqs, max_seq_len, num_kv_heads, head_dim, DX_BF16);
+  const int64_t need = key_mask ? dx_attn_prefill_masked_workspace(num_seqs, max_seq_len, num_kv_heads, head_dim,
+                                                                   DX_BF16)
+                                : vt_bytes;
   REQUIRE(workspace && aligned16(workspace), "attention: bf16 needs a 16-byte aligned workspace");
   REQUIRE(workspace_bytes >= need, "attention: workspace of %ld bytes, need %ld", (long)workspace_bytes, (long)need);
   uint16_t *vt = static_cast<uint16_t *>(workspace);
@@ -123,10 +160,44 @@ int dx_attn_prefill(const void *q, const void *k, const void *v, void *out, cons
                                        num_seqs, max_seq_len, num_kv_heads, head_dim, v_row_stride, vt_ld,
                                        as_stream(stream));
   if (e != hipSuccess) return check_launch(e, "transpose_v launch");
+  if (key_mask) {
+    uint32_t *bits = reinterpret_cast<uint32_t *>(static_cast<char *>(workspace) + align_up(vt_bytes, 256));
+    a.key_words = key_mask_words(max_seq_len);
+    e = dx_pack_key_bits_launch(key_mask, seq_start, seq_len, num_seqs, max_seq_len, a.key_words, bits,
+                                as_stream(stream));
+    if (e != hipSuccess) return check_launch(e, "key mask launch");
+    a.key_bits = bits;
+  }
   a.v = vt;
   a.v_stride = vt_ld;
   a.vt_seq_stride = seq_stride;
   return check_launch(dx_attn_bf16(a, as_stream(stream)), "attention bf16 launch");
+}
+
+}  // namespace
+
+extern "C" {
+
+int dx_attn_prefill(const void *q, const void *k, const void *v, void *out, const int32_t *seq_start,
+                    const int32_t *seq_len, int32_t num_seqs, int32_t max_seq_len, int32_t num_q_heads,
+                    int32_t num_kv_heads, int32_t head_dim, int64_t q_row_stride, int64_t k_row_stride,
+                    int64_t v_row_stride, int64_t out_row_stride, float scale, float softcap, int32_t window,
+                    int32_t causal, int32_t dtype, void *workspace, int64_t workspace_bytes, void *stream) {
+  return attn_prefill(q, k, v, nullptr, out, seq_start, seq_len, num_seqs, max_seq_len, num_q_heads, num_kv_heads,
+                      head_dim, q_row_stride, k_row_stride, v_row_stride, out_row_stride, scale, softcap, window,
+                      causal, dtype, workspace, workspace_bytes, stream);
+}
+
+int dx_attn_prefill_masked(const void *q, const void *k, const void *v, const uint8_t *key_mask, void *out,
+                           const int32_t *seq_start, const int32_t *seq_len, int32_t num_seqs, int32_t max_seq_len,
+                           int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim, int64_t q_row_stride,
+                           int64_t k_row_stride, int64_t v_row_stride, int64_t out_row_stride, float scale,
+                           float softcap, int32_t window, int32_t causal, int32_t dtype, void *workspace,
+                           int64_t workspace_bytes, void *stream) {
+  REQUIRE(key_mask, "attention: key_mask must not be null");
+  return attn_prefill(q, k, v, key_mask, out, seq_start, seq_len, num_seqs, max_seq_len, num_q_heads, num_kv_heads,
+                      head_dim, q_row_stride, k_row_stride, v_row_stride, out_row_stride, scale, softcap, window,
+                      causal, dtype, workspace, workspace_bytes, stream);
 }
 
 int dx_attn_prefill_vt(const void *q, const void *k, const void *vt, void *out, const int32_t *seq_start,
@@ -139,6 +210,8 @@ int dx_attn_prefill_vt(const void *q, const void *k, const void *vt, void *out, 
   if (st) return st;
   REQUIRE(vt_start, "attention: vt_start must not be null");
   REQUIRE(vt_ld % 8 == 0 && vt_ld > 0, "attention: vt_ld must be a positive multiple of 8");
+  st = check_bf16_ranges(max_seq_len, k_row_stride, head_dim, vt_ld);
+  if (st) return st;
   if (num_seqs == 0 || max_seq_len == 0) return DX_OK;
   AttnArgs a{q, k, vt, out, seq_start, seq_len, vt_start, num_seqs, max_seq_len, num_q_heads, num_kv_heads,
              head_dim, q_row_stride, k_row_stride, vt_ld, out_row_stride, 0, scale, softcap, window, causal ? 1 : 0};

@@ -116,13 +116,16 @@ struct Flag {
   static constexpr bool value = B;
 };
 
-template <int D, int G, int MODE>
+// KM: a per-key mask (key_bits, key_words 32-bit words per sequence; bit j of word w of sequence b is key
+// 32 w + j) hides keys beyond the causal / window rule. Every tile then takes the masked body, and a
+// query row that sees no key is written as zeros.
+template <int D, int G, int MODE, bool KM>
 __global__ void __launch_bounds__(BF_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2)))
 attn_bf16_kernel(const uint16_t *__restrict__ Q, const uint16_t *__restrict__ K, const uint16_t *__restrict__ Vt,
                  uint16_t *__restrict__ O, const int32_t *__restrict__ seq_start,
                  const int32_t *__restrict__ seq_len, const int32_t *__restrict__ vt_start, long vt_seq_stride,
                  int max_seq_len, long q_stride, long k_stride, long vt_ld, long o_stride, float scale,
-                 float softcap, int window, int causal) {
+                 float softcap, int window, int causal, const uint32_t *__restrict__ key_bits, int key_words) {
   constexpr int TK = tile_keys<D>();
   constexpr int RG = BF_WAVES / G;      // 32-row groups per head
   constexpr int BQ = 32 * RG;           // query rows per workgroup
@@ -266,9 +269,16 @@ attn_bf16_kernel(const uint16_t *__restrict__ Q, const uint16_t *__restrict__ K,
       }
       stream_sched<NKS>();  // keep only a few K fragments live at once
     }
-    // key of score r: kbase + 16 (r >> 3) + 8 lhalf + (r & 7); visible iff inside [vlo, vhi]
+    // key of score r: kbase + 16 (r >> 3) + 8 lhalf + (r & 7); visible iff inside [vlo, vhi] (and, with a
+    // key mask, its bit is set: kbase is a multiple of 32, so the block's 32 keys are one mask word)
     const int mlo = vlo - kbase - 8 * lhalf, mhi = vhi - kbase - 8 * lhalf;
-    auto keep = [&](int r) { return 16 * (r >> 3) + (r & 7) >= mlo && 16 * (r >> 3) + (r & 7) <= mhi; };
+    uint32_t kbits = 0xffffffffu;
+    if constexpr (KM && M) kbits = key_bits[(long)b * key_words + (kbase >> 5)] >> (8 * lhalf);
+    auto keep = [&](int r) {
+      const int j = 16 * (r >> 3) + (r & 7);
+      if constexpr (KM) return j >= mlo && j <= mhi && ((kbits >> j) & 1u);
+      else return j >= mlo && j <= mhi;
+    };
     if constexpr (MODE == MODE_FIXED) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
@@ -343,7 +353,7 @@ attn_bf16_kernel(const uint16_t *__restrict__ Q, const uint16_t *__restrict__ K,
   // without any mask code. The tiles before and after take the masked body. Every wave runs one
   // iteration (one barrier) per tile, whichever body.
   int ta = kt1, tb = kt1;
-  if (qw1 < len) {
+  if (!KM && qw1 < len) {
     int lo_u = 0, hi_u = len - 32;  // first / last kbase of an unmasked block
     if (causal) {
       hi_u = min(hi_u, qw0 - 31);
@@ -377,7 +387,8 @@ attn_bf16_kernel(const uint16_t *__restrict__ Q, const uint16_t *__restrict__ K,
 
   lsum += __shfl_xor(lsum, 32, 64);
   if (qi < len) {
-    const float inv = 1.f / lsum;
+    float inv = 1.f / lsum;
+    if constexpr (KM) inv = lsum > 0.f ? inv : 0.f;
     uint16_t *op = O + (start + qi) * o_stride + (long)h * D + lhalf * 4;
 #pragma unroll
     for (int db = 0; db < NDB; ++db)
@@ -397,7 +408,7 @@ __global__ void __launch_bounds__(THREADS)
 attn_f32_kernel(const float *__restrict__ Q, const float *__restrict__ K, const float *__restrict__ V,
                 float *__restrict__ O, const int32_t *__restrict__ seq_start, const int32_t *__restrict__ seq_len,
                 int max_seq_len, int hq, int hkv, long q_stride, long k_stride, long v_stride, long o_stride,
-                float scale, float softcap, int window, int causal) {
+                float scale, float softcap, int window, int causal, const uint8_t *__restrict__ key_mask) {
   constexpr int QPB = THREADS / TPQ;
   constexpr int DPT = D / TPQ;
   constexpr int TK = 32;
@@ -453,7 +464,8 @@ attn_f32_kernel(const float *__restrict__ Q, const float *__restrict__ K, const 
       for (int off = 1; off < TPQ; off <<= 1) s += __shfl_xor(s, off, 64);
       s *= scale;
       if (softcap > 0.f) s = softcap * tanhf(s / softcap);
-      const bool v = visible(qi, k0 + j, len, window, causal);
+      // key_mask (nullable) hides keys of row start + key; read only for keys inside the sequence
+      const bool v = visible(qi, k0 + j, len, window, causal) && (!key_mask || key_mask[start + k0 + j]);
       vis |= (uint32_t)v << j;
       sc[j] = s;
       if (v) tmax = fmaxf(tmax, s);
@@ -475,7 +487,7 @@ attn_f32_kernel(const float *__restrict__ Q, const float *__restrict__ K, const 
   if (qi < len) {
     float *op = O + (start + qi) * o_stride + (long)h * D + part * DPT;
 #pragma unroll
-    for (int d = 0; d < DPT; ++d) op[d] = o[d] / l;
+    for (int d = 0; d < DPT; ++d) op[d] = l > 0.f ? o[d] / l : 0.f;  // a row that sees no key: zeros
   }
 }
 
@@ -542,11 +554,13 @@ hipError_t launch_bf16_dg(const AttnArgs &a, hipStream_t s) {
   const unsigned ntiles = (a.max_seq_len + BQ - 1) / BQ;
   const dim3 grid = a.max_seq_len <= SHORT_SEQ ? dim3(a.hkv, a.num_seqs, ntiles) : dim3(ntiles, a.hkv, a.num_seqs);
   const bool fixed = a.softcap > 0.f && a.softcap <= 56.f;
-  auto kern = fixed ? attn_bf16_kernel<D, G, MODE_FIXED> : attn_bf16_kernel<D, G, MODE_ONLINE>;
+  auto kern = a.key_bits ? (fixed ? attn_bf16_kernel<D, G, MODE_FIXED, true> : attn_bf16_kernel<D, G, MODE_ONLINE, true>)
+                         : (fixed ? attn_bf16_kernel<D, G, MODE_FIXED, false> : attn_bf16_kernel<D, G, MODE_ONLINE, false>);
   kern<<<grid, dim3(BF_THREADS), 0, s>>>(
       static_cast<const uint16_t *>(a.q), static_cast<const uint16_t *>(a.k), static_cast<const uint16_t *>(a.v),
       static_cast<uint16_t *>(a.out), a.seq_start, a.seq_len, a.vt_start, a.vt_seq_stride, a.max_seq_len,
-      a.q_stride, a.k_stride, a.v_stride, a.out_stride, a.scale, a.softcap, a.window, a.causal);
+      a.q_stride, a.k_stride, a.v_stride, a.out_stride, a.scale, a.softcap, a.window, a.causal, a.key_bits,
+      a.key_words);
   return hipGetLastError();
 }
 
@@ -567,11 +581,38 @@ hipError_t launch_f32_d(const AttnArgs &a, hipStream_t s) {
   attn_f32_kernel<D, TPQ><<<grid, dim3(THREADS), 0, s>>>(
       static_cast<const float *>(a.q), static_cast<const float *>(a.k), static_cast<const float *>(a.v),
       static_cast<float *>(a.out), a.seq_start, a.seq_len, a.max_seq_len, a.hq, a.hkv, a.q_stride, a.k_stride,
-      a.v_stride, a.out_stride, a.scale, a.softcap, a.window, a.causal);
+      a.v_stride, a.out_stride, a.scale, a.softcap, a.window, a.causal, a.key_mask);
   return hipGetLastError();
 }
 
+// Thread t packs word t % words of sequence t / words: bit j <- key_mask[seq_start + 32 w + j] != 0 for keys
+// inside the sequence, 0 past its length.
+__global__ void __launch_bounds__(THREADS)
+pack_key_bits_kernel(const uint8_t *__restrict__ key_mask, const int32_t *__restrict__ seq_start,
+                     const int32_t *__restrict__ seq_len, int num_seqs, int max_seq_len, int words,
+                     uint32_t *__restrict__ bits) {
+  const long t = (long)blockIdx.x * THREADS + threadIdx.x;
+  if (t >= (long)num_seqs * words) return;
+  const int b = (int)(t / words), w = (int)(t % words);
+  const int len = min(max(seq_len[b], 0), max_seq_len);
+  const long start = seq_start[b];
+  uint32_t word = 0;
+  for (int j = 0; j < 32; ++j) {
+    const int key = 32 * w + j;
+    if (key < len && key_mask[start + key]) word |= 1u << j;
+  }
+  bits[t] = word;
+}
+
 }  // namespace
+
+hipError_t dx_pack_key_bits_launch(const uint8_t *key_mask, const int32_t *seq_start, const int32_t *seq_len,
+                                   int num_seqs, int max_seq_len, int words, uint32_t *bits, hipStream_t s) {
+  const long total = (long)num_seqs * words;
+  pack_key_bits_kernel<<<dim3((unsigned)((total + THREADS - 1) / THREADS)), dim3(THREADS), 0, s>>>(
+      key_mask, seq_start, seq_len, num_seqs, max_seq_len, words, bits);
+  return hipGetLastError();
+}
 
 hipError_t dx_attn_bf16(const AttnArgs &a, hipStream_t s) {
   switch (a.d) {

@@ -41,10 +41,15 @@ struct AttnArgs {
   long vt_seq_stride;                              // used when vt_start == nullptr
   float scale, softcap;
   int window, causal;
+  const uint8_t *key_mask = nullptr;   // fp32 path: per key row, nullable
+  const uint32_t *key_bits = nullptr;  // bf16 path: key_words bits-words per sequence, nullable
+  int key_words = 0;
 };
 
 hipError_t dx_attn_bf16(const AttnArgs &a, hipStream_t s);
 hipError_t dx_attn_f32(const AttnArgs &a, hipStream_t s);
+hipError_t dx_pack_key_bits_launch(const uint8_t *key_mask, const int32_t *seq_start, const int32_t *seq_len,
+                                   int num_seqs, int max_seq_len, int words, uint32_t *bits, hipStream_t s);
 hipError_t dx_transpose_v_launch(const uint16_t *v, uint16_t *vt, const int32_t *seq_start, const int32_t *seq_len,
                                  const int32_t *vt_start, long vt_seq_stride, int num_seqs, int max_seq_len, int hkv,
                                  int d, long v_stride, long vt_ld, hipStream_t s);

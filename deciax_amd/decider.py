@@ -19,18 +19,36 @@ from typing import Any, Literal
 from deciax_amd import gemma
 from deciax_amd.backend import ImplChoice, resolve
 from deciax_amd.engine import DecisionEngine
-from deciax_amd.schema import ByteTokenizer, TokenizerLike
+from deciax_amd.schema import MAX_TOKENS, ByteTokenizer, TokenizerLike
 
 DtypeChoice = Literal["auto", "bf16", "fp32"]
 ModelName = Literal["gemma2-9b", "gemma2-27b", "tiny"]
 
 
-class Decider:
-    """One loaded model bound to its engine (src/deciax/decider.py:22-52)."""
+class GemmaDecisionModel:
+    """A loaded Gemma-2-shaped decision model: device weights plus tokenizer. It satisfies the
+    reference's `RequestModel` protocol (src/deciax/models/base.py:58-59): `build_engine()` returns
+    the request engine that `Decider` drives, as `ClefModel` does for the reference's Clef
+    checkpoints (src/deciax/decider.py:25-27)."""
 
-    def __init__(self, engine: DecisionEngine) -> None:
-        self.engine = engine
-        self.model = engine.weights
+    def __init__(self, weights: gemma.DecisionWeights, tokenizer: TokenizerLike, name: str) -> None:
+        self.weights = weights
+        self.tokenizer = tokenizer
+        self.name = name
+        self.config = weights.config
+        self.max_token_budget = min(MAX_TOKENS, weights.config.max_position)
+
+    def build_engine(self) -> DecisionEngine:
+        return DecisionEngine(self.weights, self.tokenizer, self.name)
+
+
+class Decider:
+    """One loaded model bound to a runtime engine (src/deciax/decider.py:22-52): the engine comes
+    from `model.build_engine()`, as in the reference."""
+
+    def __init__(self, model: GemmaDecisionModel) -> None:
+        self.model = model
+        self.engine = model.build_engine()
 
     def decide(self, state: Any, questions: Mapping[Any, Mapping[str, Any]], *, max_len: int | None = None,
                head_max_len: int | None = None) -> dict[str, Any]:
@@ -74,4 +92,4 @@ def load(model: ModelName | str | Path = "gemma2-9b", *, revision: str | None = 
         config = replace(config, layers=layers)
     weights = gemma.weights_from_host(config, host) if host is not None else gemma.random_weights(config, seed=seed)
     tok = tokenizer if tokenizer is not None else ByteTokenizer(config.vocab)
-    return Decider(DecisionEngine(weights, tok, config.name if is_dir else model))
+    return Decider(GemmaDecisionModel(weights, tok, config.name if is_dir else str(model)))

@@ -29,7 +29,7 @@ so no compute is spent on padding.
 from __future__ import annotations
 
 import math
-from collections.abc import Sequence
+from collections.abc import Callable, Sequence
 from dataclasses import dataclass, field
 
 import numpy as np
@@ -159,21 +159,26 @@ class DecisionWeights:
 
     def numpy_weights(self) -> dict[str, np.ndarray]:
         """Host fp32 copies in the oracle's naming (for parity tests; needs unpacked gate/up)."""
-        c = self.config
         out = {"embed": _to_np(self.embed), "final_norm": _to_np(self.final_norm)}
-        qd, kd = c.heads * c.head_dim, c.kv_heads * c.head_dim
-        for i, lw in enumerate(self.layers):
-            if lw.gate is None or lw.up is None:
-                raise ValueError("weights were built without keep_unpacked=True")
-            qkv = _to_np(lw.qkv)
-            p = f"layers.{i}."
-            out.update({
-                p + "input_norm": _to_np(lw.input_norm), p + "q": qkv[:qd], p + "k": qkv[qd:qd + kd],
-                p + "v": qkv[qd + kd:], p + "o": _to_np(lw.o), p + "post_attn_norm": _to_np(lw.post_attn_norm),
-                p + "pre_ffn_norm": _to_np(lw.pre_ffn_norm), p + "gate": _to_np(lw.gate), p + "up": _to_np(lw.up),
-                p + "down": _to_np(lw.down), p + "post_ffn_norm": _to_np(lw.post_ffn_norm),
-            })
+        for i in range(len(self.layers)):
+            out.update({f"layers.{i}.{k}": v for k, v in self.numpy_layer(i).items()})
         return out
+
+    def numpy_layer(self, i: int) -> dict[str, np.ndarray]:
+        """Host fp32 copies of layer i's weights under the oracle's per-layer names (one layer at a
+        time, so a parity test can stream a deep model through host memory)."""
+        c = self.config
+        lw = self.layers[i]
+        if lw.gate is None or lw.up is None:
+            raise ValueError("weights were built without keep_unpacked=True")
+        qd, kd = c.heads * c.head_dim, c.kv_heads * c.head_dim
+        qkv = _to_np(lw.qkv)
+        return {
+            "input_norm": _to_np(lw.input_norm), "q": qkv[:qd], "k": qkv[qd:qd + kd], "v": qkv[qd + kd:],
+            "o": _to_np(lw.o), "post_attn_norm": _to_np(lw.post_attn_norm), "pre_ffn_norm": _to_np(lw.pre_ffn_norm),
+            "gate": _to_np(lw.gate), "up": _to_np(lw.up), "down": _to_np(lw.down),
+            "post_ffn_norm": _to_np(lw.post_ffn_norm),
+        }
 
 
 def _to_np(t: torch.Tensor) -> np.ndarray:
@@ -385,9 +390,12 @@ def layer_forward(w: DecisionWeights, i: int, batch: PackedBatch, ws: Workspace)
     K.add_rmsnorm(y, x, eps=c.eps, post_w=lw.post_ffn_norm, next_w=nxt, h=h if nxt is not None else None)
 
 
-def forward(w: DecisionWeights, batch: PackedBatch, ws: Workspace | None = None,
-            layers: int | None = None) -> tuple[torch.Tensor, torch.Tensor]:
-    """Decision forward: (option logits [O] fp32, per-question probabilities [O] fp32)."""
+def forward(w: DecisionWeights, batch: PackedBatch, ws: Workspace | None = None, layers: int | None = None,
+            on_layer: Callable[[int, torch.Tensor], None] | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """Decision forward: (option logits [O] fp32, per-question probabilities [O] fp32).
+
+    `on_layer(i, x)`, when given, sees the residual stream x [rows, H] after the embedding (i = 0)
+    and after each layer i (i = 1..L), on the current stream (parity tests read it layer by layer)."""
     c = w.config
     if batch.max_len > c.max_position:
         raise ValueError(f"request of {batch.max_len} tokens exceeds max_position {c.max_position}")
@@ -397,8 +405,12 @@ def forward(w: DecisionWeights, batch: PackedBatch, ws: Workspace | None = None,
     x, h = ws.x[:rows], ws.h[:rows]
     K.embed(batch.ids, w.embed, scale=embed_scale(c.hidden), norm_w=w.layers[0].input_norm, eps=c.eps, x=x, h=h)
     K.vt_zero_tails(ws.vt[:, :batch.vt_ld], batch.seq_len, batch.vt_start)
+    if on_layer is not None:
+        on_layer(0, x)
     n = c.layers if layers is None else layers
     for i in range(n):
         layer_forward(w, i, batch, ws)
+        if on_layer is not None:
+            on_layer(i + 1, x)
     return K.readout(x, w.final_norm, w.embed, batch.opt_pos, batch.opt_label, batch.q_offsets, eps=c.eps,
                      softcap=c.final_softcap)

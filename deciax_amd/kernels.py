@@ -48,6 +48,18 @@ def _rows(t: torch.Tensor, name: str) -> int:
     return t.stride(0)
 
 
+def _check_heads(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, hq: int, hkv: int, d: int) -> None:
+    if q.shape[1] < hq * d or k.shape[1] < hkv * d or v.shape[1] < hkv * d:
+        raise ValueError("attention: q / k / v rows narrower than heads * head_dim")
+    if not q.shape[0] == k.shape[0] == v.shape[0]:
+        raise ValueError("attention: q, k and v need the same number of rows")
+
+
+def _check_out(out: torch.Tensor, q: torch.Tensor, width: int) -> None:
+    if out.shape[0] < q.shape[0] or out.shape[1] < width:
+        raise ValueError(f"attention: out must hold [{q.shape[0]}, {width}], got {tuple(out.shape)}")
+
+
 def _activation(act: str) -> int:
     try:
         return ACTIVATIONS[act]
@@ -135,6 +147,8 @@ def gated_linear(x: torch.Tensor, gate_up: torch.Tensor, activation: str = "gelu
     if out is None:
         out = torch.empty((m, f), dtype=BF16, device=x.device)
     _need(out, "out", BF16, 2)
+    if out.shape[0] < m or out.shape[1] < f:
+        raise ValueError(f"gated_linear: out must hold [{m}, {f}], got {tuple(out.shape)}")
     call("dx_gated_linear", _ptr(x), _ptr(gate_up), _ptr(out), m, f, k, _rows(x, "x"), _rows(out, "out"),
          _activation(activation), _stream())
     return out
@@ -197,8 +211,13 @@ def rmsnorm(x: torch.Tensor, w: torch.Tensor, *, eps: float, out: torch.Tensor |
     _need(x, "x", BF16, 2)
     _need(w, "w", BF16, 1)
     rows, d = x.shape
+    if w.shape[0] != d:
+        raise ValueError(f"rmsnorm: w must be [{d}], got {tuple(w.shape)}")
     if out is None:
         out = torch.empty_like(x)
+    _need(out, "out", BF16, 2)
+    if tuple(out.shape) != (rows, d):
+        raise ValueError(f"rmsnorm: out must be [{rows}, {d}], got {tuple(out.shape)}")
     call("dx_rmsnorm", _ptr(x), _ptr(w), _ptr(out), rows, d, _rows(x, "x"), _rows(out, "out"), float(eps), _stream())
     return out
 
@@ -287,9 +306,13 @@ def attention_varlen(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, seq_star
         _need(t, n, dtype, 2)
     _need(seq_start, "seq_start", torch.int32, 1)
     _need(seq_len, "seq_len", torch.int32, 1)
+    if seq_start.shape != seq_len.shape:
+        raise ValueError("attention: one seq_start per seq_len")
+    _check_heads(q, k, v, num_q_heads, num_kv_heads, head_dim)
     if out is None:
         out = torch.empty((q.shape[0], num_q_heads * head_dim), dtype=dtype, device=q.device)
     _need(out, "out", dtype, 2)
+    _check_out(out, q, num_q_heads * head_dim)
     nseq = seq_start.shape[0]
     code = DX_BF16 if dtype == BF16 else DX_F32
     ws_bytes = _lib.lib().dx_attn_prefill_workspace(nseq, max_seq_len, num_kv_heads, head_dim, code)
@@ -338,8 +361,14 @@ def attention_vt(q: torch.Tensor, k: torch.Tensor, vt: torch.Tensor, seq_start: 
         _need(t, n, torch.int32, 1)
     if not seq_start.shape[0] == seq_len.shape[0] == vt_start.shape[0]:
         raise ValueError("attention_vt: seq_start, seq_len and vt_start need one entry per sequence")
+    if q.shape[1] < num_q_heads * head_dim or k.shape[1] < num_kv_heads * head_dim or k.shape[0] < q.shape[0]:
+        raise ValueError("attention_vt: q / k rows narrower than heads * head_dim or fewer key rows than queries")
+    if vt.shape[0] != num_kv_heads * head_dim:
+        raise ValueError(f"attention_vt: vt must have {num_kv_heads * head_dim} rows, got {vt.shape[0]}")
     if out is None:
         out = torch.empty((q.shape[0], num_q_heads * head_dim), dtype=BF16, device=q.device)
+    _need(out, "out", BF16, 2)
+    _check_out(out, q, num_q_heads * head_dim)
     call("dx_attn_prefill_vt", _ptr(q), _ptr(k), _ptr(vt), _ptr(out), _ptr(seq_start), _ptr(seq_len),
          _ptr(vt_start), seq_start.shape[0], max_seq_len, num_q_heads, num_kv_heads, head_dim, _rows(q, "q"),
          _rows(k, "k"), _rows(vt, "vt"), _rows(out, "out"), float(scale), float(softcap), int(window),
@@ -347,38 +376,116 @@ def attention_vt(q: torch.Tensor, k: torch.Tensor, vt: torch.Tensor, seq_start: 
     return out
 
 
-def _prefix_lengths(key_mask: torch.Tensor) -> torch.Tensor:
-    """Lengths of right-padded [B, S] masks; other masks are rejected."""
-    m = key_mask.to(torch.bool)
-    lengths = m.sum(dim=1, dtype=torch.int32)
-    pos = torch.arange(m.shape[1], device=m.device)[None, :]
-    if not bool(torch.equal(m, pos < lengths[:, None])):
-        raise ValueError("attention: key_mask must mark a prefix of each row (right padding)")
-    return lengths
+def attention_masked(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, key_mask: torch.Tensor,
+                     seq_start: torch.Tensor, seq_len: torch.Tensor, max_seq_len: int, *, num_q_heads: int,
+                     num_kv_heads: int, head_dim: int, scale: float, softcap: float = 0.0, window: int = 0,
+                     causal: bool = True, out: torch.Tensor | None = None) -> torch.Tensor:
+    """`attention_varlen` with a per-row key mask (uint8 or bool [rows]): key j of sequence s is
+    visible only where key_mask[seq_start[s] + j] is set. Query rows that see no key are written as
+    zeros (dx_attn_prefill_masked)."""
+    dtype = q.dtype
+    if dtype not in (BF16, F32):
+        raise ValueError(f"attention: dtype must be bf16 or fp32, got {dtype}")
+    for t, n in ((q, "q"), (k, "k"), (v, "v")):
+        _need(t, n, dtype, 2)
+    _need(seq_start, "seq_start", torch.int32, 1)
+    _need(seq_len, "seq_len", torch.int32, 1)
+    if seq_start.shape != seq_len.shape:
+        raise ValueError("attention: one seq_start per seq_len")
+    if key_mask.dim() != 1 or key_mask.shape[0] != k.shape[0] or key_mask.device != k.device:
+        raise ValueError("attention: key_mask must be a device tensor with one entry per key row")
+    mask_u8 = key_mask.to(torch.uint8).contiguous()
+    _check_heads(q, k, v, num_q_heads, num_kv_heads, head_dim)
+    if out is None:
+        out = torch.empty((q.shape[0], num_q_heads * head_dim), dtype=dtype, device=q.device)
+    _need(out, "out", dtype, 2)
+    _check_out(out, q, num_q_heads * head_dim)
+    nseq = seq_start.shape[0]
+    code = DX_BF16 if dtype == BF16 else DX_F32
+    ws_bytes = _lib.lib().dx_attn_prefill_masked_workspace(nseq, max_seq_len, num_kv_heads, head_dim, code)
+    ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=q.device)
+    call("dx_attn_prefill_masked", _ptr(q), _ptr(k), _ptr(v), _ptr(mask_u8), _ptr(out), _ptr(seq_start),
+         _ptr(seq_len), nseq, max_seq_len, num_q_heads, num_kv_heads, head_dim, _rows(q, "q"), _rows(k, "k"),
+         _rows(v, "v"), _rows(out, "out"), float(scale), float(softcap), int(window), int(bool(causal)), code,
+         _ptr(ws), ws.numel(), _stream())
+    return out
+
+
+def _visible_counts(mask: torch.Tensor, nq: int, causal: bool, window: int) -> torch.Tensor:
+    """[B, K] key mask -> [B, nq] number of keys each query row sees (index bookkeeping for the rows
+    that see none)."""
+    b, nk = mask.shape
+    cs = torch.nn.functional.pad(torch.cumsum(mask.to(torch.int32), dim=1), (1, 0))  # cs[:, j] = keys < j
+    i = torch.arange(nq, device=mask.device)
+    if causal:
+        hi = torch.clamp(i + 1, max=nk)
+        lo = torch.clamp(i - window + 1, min=0) if window > 0 else torch.zeros_like(i)
+    elif window > 0:
+        hi = torch.clamp(i + window + 1, max=nk)
+        lo = torch.clamp(i - window, min=0)
+    else:
+        hi = torch.full_like(i, nk)
+        lo = torch.zeros_like(i)
+    lo = torch.minimum(lo, hi)
+    return cs[:, hi] - cs[:, lo]
 
 
 def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, key_mask: torch.Tensor, *, causal: bool = False,
               window: int = 0, softcap: float = 0.0, scale: float | None = None) -> torch.Tensor:
-    """[B, S, H, D] q and [B, S, Hkv, D] k, v with a right-padded [B, S] key mask -> [B, S, H, D].
+    """[B, Q, H, D] queries against [B, K, Hkv, D] keys and values with a [B, K] key mask ->
+    [B, Q, H, D]: the interface of `blocked.attention` (src/deciax/kernels/attention/blocked.py:9-32)
+    and, with `causal=False` and a symmetric `window`, of `ops.attention`
+    (src/deciax/ops/__init__.py:10-26, src/deciax/kernels/attention/reference.py:11-42).
 
-    The interface of `blocked.attention` (src/deciax/kernels/attention/blocked.py:9) and, with
-    `causal=False`, of `ops.attention` (src/deciax/ops/__init__.py:10-26): rows past a sequence's
-    length are left zero (the reference computes them but never reads them,
-    tests/kernels/test_attention.py:42)."""
+    Any mask is accepted (blocked.py:23-27): masked keys get no weight. Causal visibility compares
+    row indices, key j <= query i, as blocked.py:25 does. Every query row is computed, padded ones
+    included. A row that sees no key at all gets what the reference's finite MASK_FILL gives it:
+    the uniform average of all K values (softmax of K equal scores)."""
     if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
-        raise ValueError("attention: q, k, v must be [B, S, H, D]")
-    b, s, hq, d = q.shape
-    hkv = k.shape[2]
-    if k.shape != (b, s, hkv, d) or v.shape != k.shape or key_mask.shape != (b, s):
+        raise ValueError("attention: q must be [B, Q, H, D] and k, v [B, K, Hkv, D]")
+    b, nq, hq, d = q.shape
+    nk, hkv = k.shape[1], k.shape[2]
+    if k.shape != (b, nk, hkv, d) or v.shape != k.shape or tuple(key_mask.shape) != (b, nk):
         raise ValueError("attention: inconsistent q/k/v/mask shapes")
-    lengths = _prefix_lengths(key_mask.to(q.device))
-    starts = torch.arange(b, device=q.device, dtype=torch.int32) * s
-    out = torch.zeros((b * s, hq * d), dtype=q.dtype, device=q.device)
-    attention_varlen(q.reshape(b * s, hq * d).contiguous(), k.reshape(b * s, hkv * d).contiguous(),
-                     v.reshape(b * s, hkv * d).contiguous(), starts, lengths, s, num_q_heads=hq, num_kv_heads=hkv,
-                     head_dim=d, scale=d ** -0.5 if scale is None else scale, softcap=softcap, window=window,
-                     causal=causal, out=out)
-    return out.reshape(b, s, hq, d)
+    if q.dtype not in (BF16, F32) or k.dtype != q.dtype or v.dtype != q.dtype:
+        raise ValueError("attention: q, k, v must share one dtype, bf16 or fp32")
+    if window < 0:
+        raise ValueError("attention: window must be >= 0")
+    scale = d ** -0.5 if scale is None else scale
+    mask = key_mask.to(device=q.device, dtype=torch.bool)
+    length = max(nq, nk)
+    if nk == 0:
+        raise ValueError("attention: need at least one key")
+    # One sequence per batch row of `length` rows: queries padded past Q (dropped afterwards), keys
+    # padded past K (masked out).
+    qp = torch.zeros((b, length, hq, d), dtype=q.dtype, device=q.device)
+    kp = torch.zeros((b, length, hkv, d), dtype=q.dtype, device=q.device)
+    vp = torch.zeros_like(kp)
+    mp = torch.zeros((b, length), dtype=torch.bool, device=q.device)
+    qp[:, :nq], kp[:, :nk], vp[:, :nk], mp[:, :nk] = q, k, v, mask
+    starts = torch.arange(b, device=q.device, dtype=torch.int32) * length
+    lengths = torch.full((b,), length, device=q.device, dtype=torch.int32)
+    rows = b * length
+    flat = dict(num_q_heads=hq, num_kv_heads=hkv, head_dim=d, scale=scale, softcap=softcap, window=window,
+                causal=causal)
+    args = (qp.reshape(rows, hq * d), kp.reshape(rows, hkv * d), vp.reshape(rows, hkv * d))
+    if bool(mp.all()):
+        out = attention_varlen(*args, starts, lengths, length, **flat)
+    else:
+        out = attention_masked(*args, mp.reshape(rows), starts, lengths, length, **flat)
+    out = out.reshape(b, length, hq, d)[:, :nq]
+    empty = _visible_counts(mask, nq, causal, window) == 0
+    if bool(empty.any()):
+        # softmax over K equal scores: the average of every value row, which the kernel computes for a
+        # zero query attending all K keys
+        kz = torch.zeros((b * nk, hq * d), dtype=q.dtype, device=q.device)
+        uniform = attention_varlen(kz, k.reshape(b * nk, hkv * d).contiguous(), v.reshape(b * nk, hkv * d).contiguous(),
+                                   torch.arange(b, device=q.device, dtype=torch.int32) * nk,
+                                   torch.full((b,), nk, device=q.device, dtype=torch.int32), nk, num_q_heads=hq,
+                                   num_kv_heads=hkv, head_dim=d, scale=scale, causal=False)
+        uniform = uniform.reshape(b, nk, hq, d)[:, :1].expand(b, nq, hq, d)
+        out = torch.where(empty[:, :, None, None], uniform, out)
+    return out.contiguous()
 
 
 # ---------------------------------------------------------------------------- readout
@@ -394,6 +501,16 @@ def readout(hidden: torch.Tensor, norm_w: torch.Tensor, table: torch.Tensor, opt
     for t, n in ((opt_pos, "opt_pos"), (opt_label, "opt_label"), (q_offsets, "q_offsets")):
         _need(t, n, torch.int32, 1)
     nopt = opt_pos.shape[0]
+    d = hidden.shape[1]
+    if opt_label.shape[0] != nopt:
+        raise ValueError("readout: one label per option position")
+    if norm_w.shape[0] != d or table.shape[1] != d:
+        raise ValueError(f"readout: norm_w and table rows must have {d} entries")
+    if q_offsets.shape[0] < 1:
+        raise ValueError("readout: q_offsets needs at least one entry")
+    offs = q_offsets.cpu()
+    if int(offs[0]) != 0 or int(offs[-1]) != nopt or bool((offs[1:] < offs[:-1]).any()):
+        raise ValueError("readout: q_offsets must rise monotonically from 0 to the number of options")
     logits = torch.empty(nopt, dtype=F32, device=hidden.device)
     probs = torch.empty(nopt, dtype=F32, device=hidden.device)
     nq = q_offsets.shape[0] - 1
@@ -415,8 +532,18 @@ def layer_norm_f32(x: torch.Tensor, w: torch.Tensor, b: torch.Tensor | None, *, 
                    out: torch.Tensor | None = None) -> torch.Tensor:
     """Row LayerNorm in fp32 (`layer_norm`, src/deciax/nn.py:22-29)."""
     _f32(x, "x")
+    d = x.shape[1]
+    for t, n in ((w, "w"), (b, "b")):
+        if t is not None:
+            _f32(t, n, 1)
+            if t.shape[0] != d:
+                raise ValueError(f"layer_norm_f32: {n} must be [{d}]")
+    if w is None:
+        raise ValueError("layer_norm_f32: w is required")
     out = torch.empty_like(x) if out is None else out
     _f32(out, "out")
+    if out.shape[0] < x.shape[0] or out.shape[1] < d:
+        raise ValueError(f"layer_norm_f32: out must hold {tuple(x.shape)}")
     call("dx_layer_norm_f32", _ptr(x), _ptr(w), _ptr(b), _ptr(out), x.shape[0], x.shape[1], _rows(x, "x"),
          _rows(out, "out"), float(eps), _stream())
     return out
@@ -473,8 +600,13 @@ def gather_rows_f32(x: torch.Tensor, index: torch.Tensor, *, batch: int, out: to
     _f32(x, "x")
     _need(index, "index", torch.int32, 2)
     picks = index.shape[1]
+    if index.shape[0] != batch or x.shape[0] % max(batch, 1):
+        raise ValueError("gather_rows_f32: index must be [batch, picks] and x hold batch equal row blocks")
     if out is None:
         out = torch.empty((batch * picks, x.shape[1]), dtype=F32, device=x.device)
+    _f32(out, "out")
+    if out.shape[0] < batch * picks or out.shape[1] < x.shape[1]:
+        raise ValueError(f"gather_rows_f32: out must hold [{batch * picks}, {x.shape[1]}]")
     call("dx_gather_rows_f32", _ptr(x), _ptr(index), _ptr(out), batch, x.shape[0] // batch, picks, x.shape[1],
          _rows(x, "x"), _rows(out, "out"), int(accumulate), _stream())
     return out
@@ -487,6 +619,10 @@ def head_routing_f32(options: torch.Tensor, base: torch.Tensor, option_field: to
     _f32(base, "base")
     _need(option_field, "option_field", torch.int32)
     _need(option_mask, "option_mask", torch.uint8)
+    if options.shape[0] % batch or base.shape[0] % batch or options.shape[1] != base.shape[1]:
+        raise ValueError("head_routing_f32: options and base must be batch row blocks of one width")
+    if option_field.numel() != options.shape[0] or option_mask.numel() != options.shape[0]:
+        raise ValueError("head_routing_f32: one field index and one mask entry per option")
     out = torch.empty_like(base)
     call("dx_head_routing_f32", _ptr(options), _ptr(base), _ptr(option_field), _ptr(option_mask), _ptr(out), batch,
          options.shape[0] // batch, base.shape[0] // batch, base.shape[1], _stream())
@@ -499,6 +635,10 @@ def head_fields_init_f32(base: torch.Tensor, summary_norm: torch.Tensor, global_
                  (type_embedding, "type_embedding")):
         _f32(t, n)
     _need(types, "types", torch.int32)
+    if base.shape[0] % batch or summary_norm.shape != base.shape or types.numel() != base.shape[0]:
+        raise ValueError("head_fields_init_f32: base, summary_norm and types must cover batch x fields rows")
+    if global_proj.shape != (batch, base.shape[1]) or type_embedding.shape[1] != base.shape[1]:
+        raise ValueError("head_fields_init_f32: global_proj must be [batch, width] and type_embedding [types, width]")
     out = torch.empty_like(base)
     call("dx_head_fields_init_f32", _ptr(base), _ptr(summary_norm), _ptr(global_proj), _ptr(type_embedding),
          _ptr(types), _ptr(out), batch, base.shape[0] // batch, base.shape[1], type_embedding.shape[0], _stream())
@@ -513,6 +653,11 @@ def head_features_f32(fields: torch.Tensor, options: torch.Tensor, questions: to
         _f32(t, nm)
     _need(option_field, "option_field", torch.int32)
     n, width = fields.shape
+    if options.shape != fields.shape or lexical.shape[0] != n or option_field.numel() != n or n % batch:
+        raise ValueError("head_features_f32: fields, options, lexical and option_field need one row per option")
+    if questions.shape[0] % batch or global_vector.shape != (batch, questions.shape[1]) or \
+            lexical.shape[1] != questions.shape[1]:
+        raise ValueError("head_features_f32: questions [batch x fields, hidden], global_vector [batch, hidden]")
     features = torch.empty((n, 4 * width), dtype=F32, device=fields.device)
     prior = torch.empty(n, dtype=F32, device=fields.device)
     cosine = torch.empty(n, dtype=F32, device=fields.device)

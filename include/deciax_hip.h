@@ -75,7 +75,12 @@ int dx_device_arch(int device, char *buf, int buf_len);
  * {1, 2, 4}; fp32 requires head_dim in {64, 128, 256}. The bf16 path stages V
  * transposed in `workspace` (size from dx_attn_prefill_workspace with the
  * same num_seqs and max_seq_len; the fp32 path needs none). Every seq_len must
- * be <= max_seq_len (longer ones are cut to max_seq_len). */
+ * be <= max_seq_len (longer ones are cut to max_seq_len). The bf16 kernel
+ * addresses one sequence's K rows and one KV head's V^T rows with 32-bit byte
+ * offsets: max_seq_len * k_row_stride * 2 and ((head_dim - 1) * vt_ld +
+ * max_seq_len rounded up to 64) * 2 must stay below 2^31 (DX_ERR_UNSUPPORTED
+ * otherwise; vt_ld is the V^T leading dimension, here max_seq_len rounded up
+ * to 64 times num_seqs). */
 int dx_attn_prefill(const void *q, const void *k, const void *v, void *out,
                     const int32_t *seq_start, const int32_t *seq_len,
                     int32_t num_seqs, int32_t max_seq_len, int32_t num_q_heads,
@@ -88,6 +93,32 @@ int dx_attn_prefill(const void *q, const void *k, const void *v, void *out,
 int64_t dx_attn_prefill_workspace(int32_t num_seqs, int32_t max_seq_len,
                                   int32_t num_kv_heads, int32_t head_dim,
                                   int32_t dtype);
+
+/* dx_attn_prefill with an arbitrary key mask: key j of sequence s is visible
+ * only where key_mask[seq_start[s] + j] != 0 (uint8 per row), in addition to
+ * the causal / window rule. Replaces `attention` in
+ * src/deciax/kernels/attention/blocked.py:9-32 with its [B, K] key mask
+ * (`where(valid, scores, MASK_FILL)`, blocked.py:23-27) and the masked dense
+ * attention of src/deciax/kernels/attention/reference.py:11-42. Every query
+ * row below seq_len is computed; a row that sees no key is written as zeros
+ * (the reference returns the uniform average of all values there, an
+ * artefact of the finite MASK_FILL; the Python layer restores it). Workspace
+ * size from dx_attn_prefill_masked_workspace (V^T plus the mask as bits). */
+int dx_attn_prefill_masked(const void *q, const void *k, const void *v,
+                           const uint8_t *key_mask, void *out,
+                           const int32_t *seq_start, const int32_t *seq_len,
+                           int32_t num_seqs, int32_t max_seq_len,
+                           int32_t num_q_heads, int32_t num_kv_heads,
+                           int32_t head_dim, int64_t q_row_stride,
+                           int64_t k_row_stride, int64_t v_row_stride,
+                           int64_t out_row_stride, float scale, float softcap,
+                           int32_t window, int32_t causal, int32_t dtype,
+                           void *workspace, int64_t workspace_bytes,
+                           void *stream);
+
+int64_t dx_attn_prefill_masked_workspace(int32_t num_seqs, int32_t max_seq_len,
+                                         int32_t num_kv_heads, int32_t head_dim,
+                                         int32_t dtype);
 
 /* Same as dx_attn_prefill (bf16 only), with V already transposed: position
  * p of sequence s, kv head g, dim d at vt[(g * head_dim + d) * vt_ld +

@@ -58,21 +58,28 @@ FIXED_SHIFT_MAX_CAP = 56.0  # p = exp(t - cap/2) stays a normal fp32 / bf16 numb
 
 def attention_seq(q: np.ndarray, k: np.ndarray, v: np.ndarray, *, scale: float, softcap_value: float = 0.0,
                   window: int = 0, causal: bool = True, bf16: bool = True,
-                  query_pos: Sequence[int] | None = None, rounding: str = "flash") -> np.ndarray:
-    """One sequence: q [L, Hq, D], k/v [L, Hkv, D] (values already in the input dtype) ->
-    out [nq, Hq, D] for the query positions `query_pos` (default: all L)."""
+                  query_pos: Sequence[int] | None = None, rounding: str = "flash",
+                  key_mask: np.ndarray | None = None) -> np.ndarray:
+    """One sequence: q [Lq, Hq, D], k/v [Lk, Hkv, D] (values already in the input dtype) ->
+    out [nq, Hq, D] for the query positions `query_pos` (default: all Lq).
+
+    `key_mask` [Lk] (bool, default all true) hides keys as blocked.py:23-27 does; causal visibility
+    compares indices, key j <= query i (blocked.py:25), also when Lq != Lk. A query that sees no
+    key at all gets softmax over Lk equal MASK_FILL scores: the uniform average of every value row."""
     if rounding not in ("flash", "normalized"):
         raise ValueError(f"rounding must be 'flash' or 'normalized', got {rounding!r}")
     length, hq, d = q.shape
-    hkv = k.shape[1]
+    nk, hkv = k.shape[0], k.shape[1]
     group = hq // hkv
     qpos = np.arange(length) if query_pos is None else np.asarray(query_pos)
     out = np.zeros((len(qpos), hq, d), F32)
-    kpos = np.arange(length)
+    kpos = np.arange(nk)
+    kmask = np.ones(nk, bool) if key_mask is None else np.asarray(key_mask, bool)
     fixed = 0.0 < softcap_value <= FIXED_SHIFT_MAX_CAP
     for b0 in range(0, len(qpos), BLOCK):
         rows = qpos[b0:b0 + BLOCK]
-        ok = visible(rows, kpos, length, window, causal)
+        ok = visible(rows, kpos, nk, window, causal) & kmask[None, :]
+        empty = ~ok.any(axis=1, keepdims=True)  # every score MASK_FILL: softmax is uniform over all keys
         for h in range(hq):
             g = h // group
             scores = matmul(q[rows, h, :], k[:, g, :].T) * F32(scale)
@@ -87,6 +94,7 @@ def attention_seq(q: np.ndarray, k: np.ndarray, v: np.ndarray, *, scale: float, 
             else:
                 m = F32(0.5 * softcap_value) if fixed else scores.max(axis=1, keepdims=True)
                 p = np.where(ok, np.exp(scores - m), F32(0.0)).astype(F32)
+                p = np.where(empty, F32(1.0), p).astype(F32)
                 res = matmul(maybe(p, bf16), vg) / p.sum(axis=1, keepdims=True, dtype=acc_dtype()).astype(F32)
             out[b0:b0 + len(rows), h, :] = maybe(res.astype(F32), bf16)
     return out
@@ -94,14 +102,14 @@ def attention_seq(q: np.ndarray, k: np.ndarray, v: np.ndarray, *, scale: float, 
 
 def attention_packed(q: np.ndarray, k: np.ndarray, v: np.ndarray, seq_start: Sequence[int], seq_len: Sequence[int],
                      *, scale: float, softcap_value: float = 0.0, window: int = 0, causal: bool = True,
-                     bf16: bool = True) -> np.ndarray:
+                     bf16: bool = True, rounding: str = "flash") -> np.ndarray:
     """Packed rows: q [R, Hq, D], k/v [R, Hkv, D]; sequence s is rows [start_s, start_s + len_s).
     Rows outside every sequence stay zero."""
     out = np.zeros(q.shape, F32)
     for start, length in zip(seq_start, seq_len):
         sl = slice(start, start + length)
         out[sl] = attention_seq(q[sl], k[sl], v[sl], scale=scale, softcap_value=softcap_value, window=window,
-                                causal=causal, bf16=bf16)
+                                causal=causal, bf16=bf16, rounding=rounding)
     return out
 
 

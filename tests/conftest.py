@@ -33,6 +33,16 @@ def pytest_collection_modifyitems(config: pytest.Config, items: list[pytest.Item
             item.add_marker(skip)
 
 
+def pytest_terminal_summary(terminalreporter, exitstatus: int, config: pytest.Config) -> None:
+    """Print the measured decision-forward parity numbers (tests/forward_parity.py) after the run, so
+    that they appear in the log of a quiet (-q) run as well."""
+    records = getattr(sys.modules.get("tests.forward_parity"), "RECORDS", None)
+    if records:
+        terminalreporter.write_sep("-", "decision-forward parity, measured")
+        for line in records:
+            terminalreporter.write_line(line)
+
+
 def rng(seed: int = 0) -> np.random.Generator:
     return np.random.Generator(np.random.PCG64(seed))
 

@@ -86,3 +86,26 @@ def test_attention_grid_limits() -> None:
         assert b"launch grid" in lib().dx_last_error()
     check("dx_transpose_v", _lib.DX_ERR_UNSUPPORTED, P, P, P, P, P, 70000, 64, 2, 128, 256, 4096, NUL)
     check("dx_transpose_v", _lib.DX_OK, P, P, P, P, P, 0, 64, 2, 128, 256, 4096, NUL)
+
+
+def test_attention_32bit_ranges_refused() -> None:
+    """The bf16 kernel's K and V^T buffer ranges are 32-bit: spans of 2 GiB or more are refused
+    before any launch instead of wrapping."""
+    f = ctypes.c_float
+
+    def vt(maxlen, k_stride, vt_ld, d=256):
+        return status("dx_attn_prefill_vt", P, P, P, P, P, P, P, 1, maxlen, 16, 8, d, 8192, k_stride, vt_ld, 4096,
+                      f(0.0625), f(50.0), 0, 1, NUL)
+
+    for args in ((16384, 1 << 16, 16384),    # 16384 keys x 64K-element rows = 2 GiB of K
+                 (64, 2048, 1 << 23)):       # 255 x 8M-element V^T rows
+        assert vt(*args) == _lib.DX_ERR_UNSUPPORTED
+        assert b"2 GiB" in lib().dx_last_error()
+
+    def packed(nseq, maxlen, d=256):
+        return status("dx_attn_prefill", P, P, P, P, P, P, nseq, maxlen, 16, 8, d, 4096, 2048, 2048, 4096,
+                      f(0.0625), f(50.0), 0, 1, _lib.DX_BF16, P, 1 << 40, NUL)
+
+    # V^T of 2048 sequences x 4096 keys per KV head row: (D - 1) x 8M columns x 2 bytes > 2 GiB
+    assert packed(2048, 4096) == _lib.DX_ERR_UNSUPPORTED
+    assert b"2 GiB" in lib().dx_last_error()

@@ -1,6 +1,7 @@
 """The HIP path against the committed golden fixtures (tests/golden/): attention within 2e-2 of the
-oracle's bf16 output, and the micro-model decision forward within the decision bar of the
-oracle's exactly summed probabilities (1e-3 absolute, identical argmax)."""
+oracle's bf16 output, and the micro-model decision forward checked layer by layer and at the readout
+(tests/forward_parity.py), with the same argmax as the fixture's exactly summed probabilities
+wherever their top-2 gap exceeds twice the fp32 oracle's drift from them."""
 
 from __future__ import annotations
 
@@ -10,6 +11,7 @@ import numpy as np
 import pytest
 
 from tests.conftest import i32, say, to_np
+from tests.forward_parity import check_forward
 
 pytestmark = pytest.mark.gpu
 GOLDEN = Path(__file__).resolve().parent / "golden"
@@ -50,7 +52,7 @@ def test_micro_forward_matches_golden() -> None:
                             MICRO.intermediate, MICRO.vocab, window=MICRO.window, query_pre_attn_scalar=128.0,
                             max_position=256)
     assert cfg.query_scale == MICRO.query_scale
-    w = gemma.weights_from_host(cfg, micro_weights(int(g["seed"])))
+    w = gemma.weights_from_host(cfg, micro_weights(int(g["seed"])), keep_unpacked=True)
     lengths = g["lengths"].tolist()
     starts = g["seq_start"].tolist()
     ids = [g["ids"][s:s + n].tolist() for s, n in zip(starts, lengths)]
@@ -63,15 +65,15 @@ def test_micro_forward_matches_golden() -> None:
         options[req].append([(int(g["opt_pos"][o] - starts[req]), int(g["opt_label"][o])) for o in range(a, c)])
     batch = gemma.pack_batch(ids, options)
     np.testing.assert_array_equal(batch.opt_pos.cpu().numpy(), g["opt_pos"])
+    check_forward("micro fixture, 2 layers", w, batch)
     logits, probs = gemma.forward(w, batch)
     torch.cuda.synchronize()
     p = probs.cpu().numpy()
-    err = float(np.abs(p - g["probs"]).max())
     floor = float(np.abs(g["probs_f32"] - g["probs"]).max())
-    say(f"micro forward: max |p - truth| = {err:.2e} (fp32 oracle {floor:.2e})")
-    assert err <= max(1e-3, 1.5 * floor)
+    say(f"micro forward: max |p - fixture truth| = {float(np.abs(p - g['probs']).max()):.2e} "
+        f"(fp32 oracle {floor:.2e})")
     for a, c in zip(q_off[:-1], q_off[1:]):
         top = np.sort(g["probs"][a:c])[::-1]
-        if top[0] - top[1] > 2e-3:
+        if c - a > 1 and top[0] - top[1] > 2 * floor:
             assert np.argmax(p[a:c]) == np.argmax(g["probs"][a:c])
     np.testing.assert_allclose(logits.cpu().numpy(), g["logits"], atol=5e-2, rtol=0)

@@ -1,14 +1,11 @@
 """Decision forward parity on the GPU.
 
-Truth is the oracle with every contraction summed exactly (fp64 accumulation) at the reference's
-bf16 rounding points. Two fp32 implementations that only sum in different orders (the GPU's MFMA
-tiles and numpy's BLAS) already disagree by a few 1e-3 in option probabilities on random-init
-models: each 1-ulp bf16 flip of a projection output perturbs every output of the next projection
-in that row by a fraction of an ulp, so flips spread layer by layer. The bar is therefore: the GPU
-is within max(1e-3, 1.5 x the fp32 oracle's own distance from truth) of truth, with identical
-argmax wherever truth's top-2 gap exceeds that bound. (The reference accepts 0.02 for bf16,
-tests/laya/test_parity.py:21,95-114, and measured 0.003 between its TPU and JAX paths,
-docs/clef-tp.md:48.)"""
+Every forward is checked by tests/forward_parity.py: each layer against the oracle on the GPU's own
+input to that layer (bf16 output tolerance), the readout of the GPU's final hidden state within
+1e-3 absolute with the same argmax, and the free-running end-to-end distance from the exactly summed
+oracle measured beside the fp32 oracle's own drift (recorded; see that module for why bf16 rounding
+noise through depth puts it above 1e-3). The 9B and 27B shapes run at full depth, 42 and 46 layers.
+"""
 
 from __future__ import annotations
 
@@ -16,6 +13,7 @@ import numpy as np
 import pytest
 
 from tests.conftest import rng, say
+from tests.forward_parity import check_forward
 
 pytestmark = pytest.mark.gpu
 
@@ -40,67 +38,21 @@ def _batch(lengths: list[int], vocab: int, questions: int, seed: int):
     return ids, options
 
 
-def _oracle(weights_np, config, batch, layers=None, acc=np.float32):
-    from oracle import model as om
-    from oracle.numerics import accumulation
-
-    shape = om.Shape(hidden=config.hidden, heads=config.heads, kv_heads=config.kv_heads, head_dim=config.head_dim,
-                     intermediate=config.intermediate, vocab=config.vocab,
-                     layers=config.layers if layers is None else layers, window=config.window,
-                     attn_softcap=config.attn_softcap, final_softcap=config.final_softcap,
-                     query_scale=config.query_scale, eps=config.eps, rope_theta=config.rope_theta,
-                     activation=config.activation)
-    ids = batch.ids.cpu().numpy()
-    starts = batch.seq_start.cpu().numpy().tolist()
-    pos = batch.positions.cpu().numpy()
-    with accumulation(acc):
-        x = om.forward(weights_np, shape, ids, starts, batch.lengths, pos)
-        return om.readout(x, weights_np["final_norm"], weights_np["embed"], batch.opt_pos.cpu().numpy(),
-                          batch.opt_label.cpu().numpy(), batch.q_offsets.cpu().numpy().tolist(), eps=config.eps,
-                          cap=config.final_softcap)
-
-
-def _check(probs: np.ndarray, weights_np, config, batch) -> None:
-    assert np.isfinite(probs).all()
-    q_offsets = batch.q_offsets.cpu().numpy()
-    _, truth = _oracle(weights_np, config, batch, acc=np.float64)
-    _, fp32 = _oracle(weights_np, config, batch, acc=np.float32)
-    floor = float(np.abs(fp32 - truth).max())
-    err = float(np.abs(probs - truth).max())
-    bound = max(1e-3, 1.5 * floor)
-    say(f"max |p_gpu - truth| = {err:.2e}; fp32 oracle vs truth = {floor:.2e}; bound {bound:.2e}")
-    assert err <= bound, f"max probability error {err:.2e} > {bound:.2e}"
-    for a, b in zip(q_offsets[:-1], q_offsets[1:]):
-        if b - a > 1:
-            top = np.sort(truth[a:b])[::-1]
-            if top[0] - top[1] > 2 * bound:
-                assert np.argmax(probs[a:b]) == np.argmax(truth[a:b])
-
-
 @pytest.mark.parametrize("lengths", [[37, 200, 129, 64], [300],
                                      [1, 2, 63, 64, 65, 127, 128, 129],  # tile, window and query-block edges
                                      [1]])
 def test_tiny_forward_matches_oracle(lengths: list[int]) -> None:
-    import torch
-
     from deciax_amd import gemma
 
     say(f"tiny decision forward lengths={lengths}")
     cfg = gemma.CONFIGS["tiny"]
     w = gemma.random_weights(cfg, seed=1, keep_unpacked=True, norm_std=0.3)
     ids, options = _batch(lengths, cfg.vocab, 4, seed=len(lengths))
-    batch = gemma.pack_batch(ids, options)
-    logits, probs = gemma.forward(w, batch)
-    torch.cuda.synchronize()
-    wn = w.numpy_weights()
-    _check(probs.cpu().numpy(), wn, cfg, batch)
-    z, _ = _oracle(wn, cfg, batch)
-    np.testing.assert_allclose(logits.cpu().numpy(), z, atol=5e-2, rtol=0)
+    check_forward(f"tiny {lengths}", w, gemma.pack_batch(ids, options))
 
 
 def test_9b_shape_two_layers_matches_oracle() -> None:
     """The 9B shape (H 3584, 16/8 x 256, MLP 14336, vocab 256000) through one sliding and one global layer."""
-    import torch
     from dataclasses import replace
 
     from deciax_amd import gemma
@@ -109,17 +61,13 @@ def test_9b_shape_two_layers_matches_oracle() -> None:
     cfg = replace(gemma.CONFIGS["gemma2-9b"], layers=2)
     w = gemma.random_weights(cfg, seed=2, keep_unpacked=True, norm_std=0.3)
     ids, options = _batch([333, 96], cfg.vocab, 8, seed=5)
-    batch = gemma.pack_batch(ids, options)
-    logits, probs = gemma.forward(w, batch)
-    torch.cuda.synchronize()
-    _check(probs.cpu().numpy(), w.numpy_weights(), cfg, batch)
+    check_forward("9b shape, 2 layers", w, gemma.pack_batch(ids, options))
 
 
 def test_27b_shape_two_layers_matches_oracle() -> None:
     """The 27B shape (H 4608, 32/16 heads x 128, query scale 1/sqrt(144), MLP 36864, vocab 256000)
     through one sliding and one global layer; one request crosses a small window so the sliding
     mask bites."""
-    import torch
     from dataclasses import replace
 
     from deciax_amd import gemma
@@ -128,10 +76,32 @@ def test_27b_shape_two_layers_matches_oracle() -> None:
     cfg = replace(gemma.CONFIGS["gemma2-27b"], layers=2, window=128)
     w = gemma.random_weights(cfg, seed=4, keep_unpacked=True, norm_std=0.3)
     ids, options = _batch([301, 77], cfg.vocab, 6, seed=9)
-    batch = gemma.pack_batch(ids, options)
-    logits, probs = gemma.forward(w, batch)
-    torch.cuda.synchronize()
-    _check(probs.cpu().numpy(), w.numpy_weights(), cfg, batch)
+    check_forward("27b shape, 2 layers, window 128", w, gemma.pack_batch(ids, options))
+
+
+@pytest.mark.parametrize("model,lengths", [("gemma2-9b", [96, 40]), ("gemma2-27b", [64, 32])])
+def test_full_depth_forward_matches_oracle(model: str, lengths: list[int]) -> None:
+    """The benchmark's shapes at full depth (9B: 42 layers, 27B: 46 layers) with the benchmark's
+    random-init distributions, on two short requests whose ids and option labels come from the first
+    4096 vocabulary rows: every layer against the oracle on the GPU's own input, the readout within
+    1e-3, and the end-to-end distance from the exactly summed oracle measured beside the fp32 oracle's."""
+    from deciax_amd import gemma
+
+    cfg = gemma.CONFIGS[model]
+    say(f"{model} full-depth decision forward lengths={lengths}")
+    w = gemma.random_weights(cfg, seed=21, keep_unpacked=True)
+    r = rng(5)
+    ids = [r.integers(0, 4096, n).tolist() for n in lengths]
+    options = []
+    for n in lengths:
+        positions = r.choice(np.arange(max(0, n - 48), n), size=min(n, 24), replace=False)
+        req, used = [], 0
+        while used + 2 <= len(positions) and len(req) < 6:
+            k = int(min(r.integers(2, 7), len(positions) - used))
+            req.append([(int(p), int(r.integers(0, 4096))) for p in positions[used:used + k]])
+            used += k
+        options.append(req)
+    check_forward(f"{model} full depth {lengths}", w, gemma.pack_batch(ids, options))
 
 
 def test_checkpoint_directory_forward_matches_oracle(tmp_path) -> None:
@@ -178,9 +148,8 @@ def test_checkpoint_directory_forward_matches_oracle(tmp_path) -> None:
     assert w.config.query_scale == cfg.query_scale and w.config.window == cfg.window
     ids, options = _batch([150, 41], cfg.vocab, 3, seed=13)
     batch = gemma.pack_batch(ids, options)
-    logits, probs = gemma.forward(w, batch)
-    torch.cuda.synchronize()
-    _check(probs.cpu().numpy(), w.numpy_weights(), w.config, batch)
+    check_forward("checkpoint directory, 2 layers", w, batch)
+    _, probs = gemma.forward(w, batch)
     _, probs_src = gemma.forward(src, batch)
     np.testing.assert_array_equal(probs.cpu().numpy(), probs_src.cpu().numpy())
     d = deciax_amd.load(str(tmp_path), impl="hip")

@@ -126,6 +126,33 @@ def test_load_validates_arguments() -> None:
         deciax_amd.load("tiny", impl="nope")  # type: ignore[arg-type]
 
 
+def test_decider_builds_its_engine_from_the_model() -> None:
+    """Decider(model) takes a RequestModel and calls model.build_engine() (src/deciax/decider.py:25-27,
+    src/deciax/models/base.py:58-59); decide/decide_batch go to that engine with the budgets."""
+    from deciax_amd.decider import Decider
+
+    calls: list[tuple[Any, ...]] = []
+
+    class Engine:
+        def decide_batch(self, states, questions, *, max_len=None, head_max_len=None):
+            calls.append((tuple(states), max_len, head_max_len))
+            return [{"state": s} for s in states]
+
+    class Model:
+        built = 0
+
+        def build_engine(self):
+            Model.built += 1
+            return Engine()
+
+    model = Model()
+    d = Decider(model)  # type: ignore[arg-type]
+    assert d.model is model and Model.built == 1
+    assert d.decide("s", {"q": {"type": "noul"}}, max_len=64) == {"state": "s"}
+    assert d.decide_batch(["a", "b"], {"q": {"type": "noul"}}) == [{"state": "a"}, {"state": "b"}]
+    assert calls == [(("s",), 64, None), (("a", "b"), None, None)]
+
+
 # ----------------------------------------------------------------------------- schema
 
 

@@ -168,3 +168,70 @@ def test_attention_flops_counts_visible_pairs() -> None:
         else:
             assert flops == 4 * 16 * 3 * (w * (w + 1) // 2 + (n - w) * w)
     assert math.isclose(attention_flops([2048] * 8, num_q_heads=16, head_dim=256), 2.750e11, rel_tol=1e-3)
+
+
+def brute_masked(q, k, v, key_mask, *, scale, window, causal):
+    """float64 loops with an arbitrary key mask and separate query / key lengths: the reference's
+    `_naive` (tests/kernels/test_attention.py:17-32: keys j with mask[j] and |i - j| <= window)
+    extended with the causal rule of blocked.py:25 (j <= i) and GQA. Rows with no key are left out
+    (None), as `_naive` leaves them."""
+    nq, hq, d = q.shape
+    nk, hkv = k.shape[0], k.shape[1]
+    out = np.zeros((nq, hq, d))
+    empty = []
+    for i in range(nq):
+        if causal:
+            keys = [j for j in range(nk) if key_mask[j] and j <= i and (window <= 0 or j > i - window)]
+        else:
+            keys = [j for j in range(nk) if key_mask[j] and (window <= 0 or abs(i - j) <= window)]
+        if not keys:
+            empty.append(i)
+            continue
+        for h in range(hq):
+            g = h // (hq // hkv)
+            s = np.array([float(np.dot(q[i, h].astype(np.float64), k[j, g].astype(np.float64))) for j in keys])
+            w = np.exp(s * scale - (s * scale).max())
+            out[i, h] = (w / w.sum()) @ v[keys, g].astype(np.float64)
+    return out, empty
+
+
+@pytest.mark.parametrize("nq,nk,causal,window", [(23, 23, True, 0), (17, 29, True, 0), (29, 17, True, 6),
+                                                 (20, 26, False, 0), (26, 20, False, 4)])
+def test_oracle_key_mask_matches_brute_force(nq, nk, causal, window) -> None:
+    r = rng(nq * 31 + nk)
+    hq, hkv, d = 4, 2, 16
+    q = r.normal(size=(nq, hq, d)).astype(np.float32)
+    k = r.normal(size=(nk, hkv, d)).astype(np.float32)
+    v = r.normal(size=(nk, hkv, d)).astype(np.float32)
+    key_mask = r.random(nk) < 0.6
+    key_mask[0] = False  # causal row 0 then sees no key
+    for rounding in ("flash", "normalized"):
+        got = attention_seq(q, k, v, scale=0.25, window=window, causal=causal, bf16=False, key_mask=key_mask,
+                            rounding=rounding)
+        want, empty = brute_masked(q, k, v, key_mask, scale=0.25, window=window, causal=causal)
+        keep = np.setdiff1d(np.arange(nq), empty)
+        np.testing.assert_allclose(got[keep], want[keep], rtol=1e-5, atol=1e-5)
+        if empty:  # softmax over nk equal MASK_FILL scores: the mean of all value rows
+            mean = np.repeat(v.astype(np.float64).mean(axis=0), hq // hkv, axis=0)
+            np.testing.assert_allclose(got[empty], np.broadcast_to(mean, (len(empty), hq, d)), rtol=1e-5, atol=1e-5)
+
+
+def test_oracle_non_prefix_mask_matches_dense_closed_form() -> None:
+    """The dense form of tests/test_qwen3_5.py:27-40 (repeat K/V, einsum, where(-1e30), softmax) with
+    a non-prefix key mask whose first keys are hidden, so the first causal rows see no key and take
+    the uniform softmax the finite MASK_FILL gives them; every row is compared."""
+    r = rng(8)
+    s, d = 139, 8
+    q = r.normal(size=(s, 4, d)).astype(np.float32)
+    k = r.normal(size=(s, 2, d)).astype(np.float32)
+    v = r.normal(size=(s, 2, d)).astype(np.float32)
+    mask = r.random(s) < 0.5
+    mask[:3] = False
+    keys, values = np.repeat(k, 2, axis=1), np.repeat(v, 2, axis=1)
+    logits = np.einsum("qhd,khd->hqk", q, keys).astype(np.float32) * np.float32(d ** -0.5)
+    causal = np.arange(s)[:, None] >= np.arange(s)[None, :]
+    logits = np.where(mask[None, None, :] & causal[None], logits, np.float32(-1e30))
+    e = np.exp(logits - logits.max(axis=-1, keepdims=True))
+    want = np.einsum("hqk,khd->qhd", e / e.sum(axis=-1, keepdims=True), values)
+    got = attention_seq(q, k, v, scale=d ** -0.5, bf16=False, key_mask=mask)
+    np.testing.assert_allclose(got, want, rtol=1e-5, atol=1e-5)
