@@ -23,6 +23,7 @@ HEADER = Path(__file__).resolve().parent.parent / "include" / "deciax_hip.h"
 DX_OK, DX_ERR_INVALID, DX_ERR_UNSUPPORTED, DX_ERR_RUNTIME = 0, 1, 2, 3
 DX_BF16, DX_F32 = 0, 1
 DX_ACT_GELU_TANH, DX_ACT_SILU, DX_ACT_GELU_ERF, DX_ACT_NONE = 0, 1, 2, 3
+DX_NOALLOC_SCRATCH_BYTES = 64 << 20
 
 _p = c_void_p
 _i32p = POINTER(c_int32)
@@ -38,6 +39,11 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
          c_float, c_float, c_int32, c_int32, c_int32, _p, c_int64, _p],
     ),
     "dx_attn_prefill_workspace": (c_int64, [c_int32, c_int32, c_int32, c_int32, c_int32]),
+    "dx_attn_prefill_noalloc": (
+        c_int,
+        [_p, _p, _p, _p, _p, _p, c_int32, c_int32, c_int32, c_int32, c_int32, c_int64, c_int64, c_int64, c_int64,
+         c_float, c_float, c_int32, c_int32, c_int32, _p],
+    ),
     "dx_attn_prefill_masked": (
         c_int,
         [_p, _p, _p, _p, _p, _p, _p, c_int32, c_int32, c_int32, c_int32, c_int32, c_int64, c_int64, c_int64,

@@ -5,6 +5,8 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <mutex>
+
 #include "common.h"
 #include "kernels.h"
 
@@ -125,14 +127,43 @@ int64_t dx_attn_prefill_masked_workspace(int32_t num_seqs, int32_t max_seq_len, 
 
 }  // extern "C"
 
+// V^T staging of dx_attn_prefill_noalloc, for callers that cannot allocate. Each GPU holds its own copy
+// from the library's first use on it until the process ends. In host code `scratch` only names the
+// array: its device address comes from hipGetSymbolAddress, once per device (scratch_on_current_device).
+static __device__ __align__(256) unsigned char scratch[DX_NOALLOC_SCRATCH_BYTES];
+
 namespace {
 
+std::mutex g_scratch_mu;
+constexpr int MAX_DEVICES = 64;
+void *g_scratch[MAX_DEVICES] = {};
+
+// Device address of the current device's `scratch`, looked up on the first call on that device.
+int scratch_on_current_device(void **out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(DX_ERR_RUNTIME, "hipGetDevice: %s", hipGetErrorString(e));
+  SUPPORTED(dev >= 0 && dev < MAX_DEVICES, "attention: device %d beyond the %d the static scratch tracks", dev,
+            MAX_DEVICES);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch[dev]) {
+    void *p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return fail(DX_ERR_RUNTIME, "hipGetSymbolAddress(scratch) on device %d: %s", dev, hipGetErrorString(e));
+    g_scratch[dev] = p;
+  }
+  *out = g_scratch[dev];
+  return DX_OK;
+}
+
+// static_scratch: stage V^T in the current device's `scratch` instead of `workspace` (which is ignored).
 int attn_prefill(const void *q, const void *k, const void *v, const uint8_t *key_mask, void *out,
                  const int32_t *seq_start, const int32_t *seq_len, int32_t num_seqs, int32_t max_seq_len,
                  int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim, int64_t q_row_stride,
                  int64_t k_row_stride, int64_t v_row_stride, int64_t out_row_stride, float scale, float softcap,
                  int32_t window, int32_t causal, int32_t dtype, void *workspace, int64_t workspace_bytes,
-                 void *stream) {
+                 void *stream, bool static_scratch = false) {
   int st = validate_attn(q, k, v, out, seq_start, seq_len, num_seqs, max_seq_len, num_q_heads, num_kv_heads,
                          head_dim, q_row_stride, k_row_stride, out_row_stride, scale, softcap, window, dtype);
   if (st) return st;
@@ -153,6 +184,14 @@ int attn_prefill(const void *q, const void *k, const void *v, const uint8_t *key
   const int64_t need = key_mask ? dx_attn_prefill_masked_workspace(num_seqs, max_seq_len, num_kv_heads, head_dim,
                                                                    DX_BF16)
                                 : vt_bytes;
+  if (static_scratch) {
+    SUPPORTED(need <= DX_NOALLOC_SCRATCH_BYTES,
+              "attention_noalloc: V^T staging of %ld bytes exceeds the %ld-byte static scratch", (long)need,
+              (long)DX_NOALLOC_SCRATCH_BYTES);
+    st = scratch_on_current_device(&workspace);
+    if (st) return st;
+    workspace_bytes = DX_NOALLOC_SCRATCH_BYTES;
+  }
   REQUIRE(workspace && aligned16(workspace), "attention: bf16 needs a 16-byte aligned workspace");
   REQUIRE(workspace_bytes >= need, "attention: workspace of %ld bytes, need %ld", (long)workspace_bytes, (long)need);
   uint16_t *vt = static_cast<uint16_t *>(workspace);
@@ -186,6 +225,16 @@ int dx_attn_prefill(const void *q, const void *k, const void *v, void *out, cons
   return attn_prefill(q, k, v, nullptr, out, seq_start, seq_len, num_seqs, max_seq_len, num_q_heads, num_kv_heads,
                       head_dim, q_row_stride, k_row_stride, v_row_stride, out_row_stride, scale, softcap, window,
                       causal, dtype, workspace, workspace_bytes, stream);
+}
+
+int dx_attn_prefill_noalloc(const void *q, const void *k, const void *v, void *out, const int32_t *seq_start,
+                            const int32_t *seq_len, int32_t num_seqs, int32_t max_seq_len, int32_t num_q_heads,
+                            int32_t num_kv_heads, int32_t head_dim, int64_t q_row_stride, int64_t k_row_stride,
+                            int64_t v_row_stride, int64_t out_row_stride, float scale, float softcap,
+                            int32_t window, int32_t causal, int32_t dtype, void *stream) {
+  return attn_prefill(q, k, v, nullptr, out, seq_start, seq_len, num_seqs, max_seq_len, num_q_heads, num_kv_heads,
+                      head_dim, q_row_stride, k_row_stride, v_row_stride, out_row_stride, scale, softcap, window,
+                      causal, dtype, nullptr, 0, stream, /*static_scratch=*/true);
 }
 
 int dx_attn_prefill_masked(const void *q, const void *k, const void *v, const uint8_t *key_mask, void *out,

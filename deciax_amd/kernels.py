@@ -376,6 +376,32 @@ def attention_vt(q: torch.Tensor, k: torch.Tensor, vt: torch.Tensor, seq_start: 
     return out
 
 
+def attention_varlen_noalloc(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, seq_start: torch.Tensor,
+                             seq_len: torch.Tensor, max_seq_len: int, *, num_q_heads: int, num_kv_heads: int,
+                             head_dim: int, scale: float, softcap: float = 0.0, window: int = 0, causal: bool = True,
+                             out: torch.Tensor) -> torch.Tensor:
+    """`attention_varlen` through dx_attn_prefill_noalloc: nothing is allocated (the caller passes
+    `out`; the bf16 path stages V^T in the library's static per-GPU scratch of
+    DX_NOALLOC_SCRATCH_BYTES). Calls that overlap on one GPU race on that scratch."""
+    dtype = q.dtype
+    if dtype not in (BF16, F32):
+        raise ValueError(f"attention: dtype must be bf16 or fp32, got {dtype}")
+    for t, n in ((q, "q"), (k, "k"), (v, "v")):
+        _need(t, n, dtype, 2)
+    _need(seq_start, "seq_start", torch.int32, 1)
+    _need(seq_len, "seq_len", torch.int32, 1)
+    if seq_start.shape != seq_len.shape:
+        raise ValueError("attention: one seq_start per seq_len")
+    _check_heads(q, k, v, num_q_heads, num_kv_heads, head_dim)
+    _need(out, "out", dtype, 2)
+    _check_out(out, q, num_q_heads * head_dim)
+    call("dx_attn_prefill_noalloc", _ptr(q), _ptr(k), _ptr(v), _ptr(out), _ptr(seq_start), _ptr(seq_len),
+         seq_start.shape[0], max_seq_len, num_q_heads, num_kv_heads, head_dim, _rows(q, "q"), _rows(k, "k"),
+         _rows(v, "v"), _rows(out, "out"), float(scale), float(softcap), int(window), int(bool(causal)),
+         DX_BF16 if dtype == BF16 else DX_F32, _stream())
+    return out
+
+
 def attention_masked(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, key_mask: torch.Tensor,
                      seq_start: torch.Tensor, seq_len: torch.Tensor, max_seq_len: int, *, num_q_heads: int,
                      num_kv_heads: int, head_dim: int, scale: float, softcap: float = 0.0, window: int = 0,

@@ -7,7 +7,8 @@
  * synchronises the host. The caller owns every buffer; entry points that need
  * scratch memory take a caller-provided workspace whose size comes from the
  * matching `*_workspace` query. Calls are thread-safe given distinct output
- * buffers (the library keeps no mutable device state).
+ * buffers; the library keeps no mutable device state, except the static
+ * scratch array of dx_attn_prefill_noalloc.
  *
  * Return value: DX_OK, or a status code; `dx_last_error()` then holds a
  * message for the calling thread. DX_ERR_INVALID and DX_ERR_UNSUPPORTED mean
@@ -93,6 +94,29 @@ int dx_attn_prefill(const void *q, const void *k, const void *v, void *out,
 int64_t dx_attn_prefill_workspace(int32_t num_seqs, int32_t max_seq_len,
                                   int32_t num_kv_heads, int32_t head_dim,
                                   int32_t dtype);
+
+/* dx_attn_prefill without a workspace: no counterpart in the reference. For
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * serving loops that forbid hipMalloc). The bf16 path stages V^T in a static
+ * device array of DX_NOALLOC_SCRATCH_BYTES that the library holds on each GPU
+ * it runs on until the process ends (its address is looked up on the first
+ * call on a device); calls whose V^T staging, dx_attn_prefill_workspace(...)
+ * bytes, exceeds it return DX_ERR_UNSUPPORTED. Nothing is allocated and
+ * nothing needs clearing: the transpose writes every V^T column the attention
+ * kernel reads. Every call on one GPU shares that GPU's array, so calls that
+ * overlap on one GPU (concurrent streams or threads) race; serialise them.
+ * Results are identical to dx_attn_prefill's. */
+#define DX_NOALLOC_SCRATCH_BYTES (64LL << 20)
+
+int dx_attn_prefill_noalloc(const void *q, const void *k, const void *v,
+                            void *out, const int32_t *seq_start,
+                            const int32_t *seq_len, int32_t num_seqs,
+                            int32_t max_seq_len, int32_t num_q_heads,
+                            int32_t num_kv_heads, int32_t head_dim,
+                            int64_t q_row_stride, int64_t k_row_stride,
+                            int64_t v_row_stride, int64_t out_row_stride,
+                            float scale, float softcap, int32_t window,
+                            int32_t causal, int32_t dtype, void *stream);
 
 /* dx_attn_prefill with an arbitrary key mask: key j of sequence s is visible
  * only where key_mask[seq_start[s] + j] != 0 (uint8 per row), in addition to

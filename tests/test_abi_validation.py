@@ -109,3 +109,17 @@ def test_attention_32bit_ranges_refused() -> None:
     # V^T of 2048 sequences x 4096 keys per KV head row: (D - 1) x 8M columns x 2 bytes > 2 GiB
     assert packed(2048, 4096) == _lib.DX_ERR_UNSUPPORTED
     assert b"2 GiB" in lib().dx_last_error()
+
+
+def test_noalloc_attention_refuses_oversize_before_any_launch() -> None:
+    """dx_attn_prefill_noalloc stages V^T in a static scratch of DX_NOALLOC_SCRATCH_BYTES; a call that
+    needs more is refused with DX_ERR_UNSUPPORTED before touching the device."""
+    f = ctypes.c_float
+    need = lib().dx_attn_prefill_workspace(64, 4096, 8, 256, _lib.DX_BF16)
+    assert need > _lib.DX_NOALLOC_SCRATCH_BYTES
+    got = status("dx_attn_prefill_noalloc", P, P, P, P, P, P, 64, 4096, 16, 8, 256, 4096, 2048, 2048, 4096,
+                 f(0.0625), f(50.0), 0, 1, _lib.DX_BF16, NUL)
+    assert got == _lib.DX_ERR_UNSUPPORTED
+    assert b"static scratch" in lib().dx_last_error()
+    check("dx_attn_prefill_noalloc", _lib.DX_OK, P, P, P, P, P, P, 0, 4096, 16, 8, 256, 4096, 2048, 2048, 4096,
+          f(0.0625), f(50.0), 0, 1, _lib.DX_BF16, NUL)
