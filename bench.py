@@ -148,13 +148,21 @@ def algorithmic_work(cfg, lengths: list[int]) -> dict[str, float]:
     }
 
 
-def algorithmic_bytes(cfg, lengths: list[int]) -> dict[str, float]:
+def readout_bytes(hidden: int, options: int, questions: int) -> float:
+    """Algorithmic bytes of one readout: per option its hidden row and its label's embedding row (bf16),
+    its position and label (int32) and its logit and probability (fp32); the norm weights once and the
+    question offsets."""
+    return options * (4.0 * hidden + 16.0) + 2.0 * hidden + 4.0 * (questions + 1)
+
+
+def algorithmic_bytes(cfg, lengths: list[int], options: int = 0, questions: int = 0) -> dict[str, float]:
     """Algorithmic HBM bytes of one average launch of the memory-bound kernels: add_rmsnorm reads y and
     the residual x and writes x and the next block's normed h, bf16 [T, H] each; the last of the 2 L
-    launches has no next norm and writes no h."""
+    launches has no next norm and writes no h. The readout as `readout_bytes`."""
     th = 2.0 * sum(lengths) * cfg.hidden
     launches = 2 * cfg.layers
-    return {"add_rmsnorm": ((launches - 1) * 4 * th + 3 * th) / launches}
+    return {"add_rmsnorm": ((launches - 1) * 4 * th + 3 * th) / launches,
+            "readout": readout_bytes(cfg.hidden, options, questions)}
 
 
 TRAFFIC_PROFILES = {("gemma2-9b", "gate_up_proj"): ROOT / "profiles" / "gate_up_gemm_traffic.md"}
@@ -240,8 +248,15 @@ def config_kernels(reps: int = 5) -> dict:
     - attention, fp32: batch 1 x 512, 8/4 heads x 128, causal, scale 128^-0.5, no softcap;
     - attention layer pair, bf16: batch 8 x 2048, 16/8 heads x 256, softcap 50, scale 1/16, the
       sliding layer (window 4096, inactive at 2048) plus the global layer; and one window-512 layer;
-    - fused MLP, bf16: 8192 rows, H 3584, I 14336, RMSNorm(1 + w) -> GELU-tanh gate|up -> down.
-    Each entry's FLOPs are algorithmic (4 D Hq per visible pair; 6 T H I), the inputs already in HBM."""
+    - the 9B attention layer pair at 8K-token prompts: batch 8 x 8192, 16/8 heads x 256, scale 1/16,
+      softcap 50, sliding window 4096 plus global; and the 27B pair at the same lengths (32/16 heads
+      x 128, scale 1/sqrt(144));
+    - fused MLP, bf16: 8192 rows, H 3584, I 14336, RMSNorm(1 + w) -> GELU-tanh gate|up -> down;
+    - the 27B readout: 2048 options (4 requests x 64 questions x 8) over 4 x 16384 rows of H 4608
+      and the 256000-row embedding table.
+    bf16 attention times the kernel on V already transposed (the forward's form, dx_attn_prefill_vt).
+    Each entry's FLOPs are algorithmic (4 D Hq per visible pair; 6 T H I), the bytes as
+    `readout_bytes`, the inputs already in HBM."""
     import torch
 
     from deciax_amd import kernels as K
@@ -267,10 +282,18 @@ def config_kernels(reps: int = 5) -> dict:
         starts = torch.arange(b, dtype=torch.int32, device="cuda") * s
         lens = torch.full((b,), s, dtype=torch.int32, device="cuda")
         o = torch.empty_like(q)
-        ms = sum(timed(lambda w=w: K.attention_varlen(q, k, v, starts, lens, s, num_q_heads=hq, num_kv_heads=hkv,
-                                                      head_dim=d, scale=scale, softcap=softcap, window=w,
-                                                      out=o)) for w in windows)
+        kw = dict(num_q_heads=hq, num_kv_heads=hkv, head_dim=d, scale=scale, softcap=softcap, out=o)
+        if dtype == torch.bfloat16:
+            padded = (s + 63) // 64 * 64
+            vt = torch.zeros((hkv * d, b * padded), dtype=dtype, device="cuda")
+            vt_start = torch.arange(b, dtype=torch.int32, device="cuda") * padded
+            K.transpose_v(v, vt, starts, lens, vt_start, s, num_kv_heads=hkv, head_dim=d)
+            run = lambda w: K.attention_vt(q, k, vt, starts, lens, vt_start, s, window=w, **kw)  # noqa: E731
+        else:
+            run = lambda w: K.attention_varlen(q, k, v, starts, lens, s, window=w, **kw)  # noqa: E731
+        ms = sum(timed(lambda w=w: run(w)) for w in windows)
         flops = sum(4.0 * d * hq * b * causal_pairs(s, w) for w in windows)
+        del q, k, v, o
         return ms, flops
 
     ms, fl = attn_case(1, 512, 8, 4, 128, torch.float32, 128 ** -0.5, 0.0, [0])
@@ -282,6 +305,11 @@ def config_kernels(reps: int = 5) -> dict:
     ms, fl = attn_case(8, 2048, 16, 8, 256, torch.bfloat16, 1 / 16, 50.0, [512])
     out["attention_window512_bf16_8x2048_16/8x256"] = {"ms": round(ms, 3), "tflops": round(fl / ms / 1e9, 2),
                                                        "frac_bf16_peak": round(fl / ms * 1e3 / PEAK_BF16, 4)}
+    for name, hq, hkv, d, scale in (("attention_layer_pair_bf16_8x8192_16/8x256", 16, 8, 256, 1 / 16),
+                                    ("attention_layer_pair_bf16_8x8192_32/16x128", 32, 16, 128, 144 ** -0.5)):
+        ms, fl = attn_case(8, 8192, hq, hkv, d, torch.bfloat16, scale, 50.0, [4096, 0])
+        out[name] = {"ms": round(ms, 3), "tflops": round(fl / ms / 1e9, 2),
+                     "frac_bf16_peak": round(fl / ms * 1e3 / PEAK_BF16, 4)}
     t, h, f = 8192, 3584, 14336
     x = torch.randn((t, h), generator=g, device="cuda").to(torch.bfloat16)
     norm = (torch.randn((h,), generator=g, device="cuda") * 0.02).to(torch.bfloat16)
@@ -291,7 +319,72 @@ def config_kernels(reps: int = 5) -> dict:
     fl = 6.0 * t * h * f
     out["mlp_bf16_8192x3584x14336"] = {"ms": round(ms, 3), "tflops": round(fl / ms / 1e9, 2),
                                        "frac_bf16_peak": round(fl / ms * 1e3 / PEAK_BF16, 4)}
+    # the 9B forward's gate|up GEMM (70471 rows, the benchmark batch) and, as a yardstick, hipBLASLt on the
+    # same product as a plain GEMM (torch.matmul, no epilogue: it writes twice the output bytes)
+    t = 70471
+    x = torch.randn((t, h), generator=g, device="cuda").to(torch.bfloat16)
+    act = torch.empty((t, f), dtype=torch.bfloat16, device="cuda")
+    fl = 2.0 * t * h * 2 * f
+    ms = timed(lambda: K.gated_linear(x, gate_up, out=act))
+    out["gemm_gate_up_bf16_70471x28672x3584"] = {"ms": round(ms, 3), "tflops": round(fl / ms / 1e9, 2),
+                                                 "frac_bf16_peak": round(fl / ms * 1e3 / PEAK_BF16, 4)}
+    del act
+    plain = torch.empty((t, 2 * f), dtype=torch.bfloat16, device="cuda")
+    ms = timed(lambda: torch.matmul(x, gate_up.t(), out=plain))
+    out["yardstick_hipblaslt_gemm_bf16_70471x28672x3584"] = {
+        "ms": round(ms, 3), "tflops": round(fl / ms / 1e9, 2), "frac_bf16_peak": round(fl / ms * 1e3 / PEAK_BF16, 4),
+        "note": "torch.matmul (hipBLASLt) plain GEMM of the same shape, a yardstick only"}
+    del x, gate_up, down, plain
+    # 27B readout: 4 requests x 16384 rows, 64 questions x 8 options in each request's last 512 rows
+    h, rows, vocab, nreq, nq, per = 4608, 4 * 16384, 256000, 4, 64, 8
+    hidden = torch.randn((rows, h), generator=g, device="cuda").to(torch.bfloat16)
+    table = (torch.randn((vocab, h), generator=g, device="cuda") * 0.02).to(torch.bfloat16)
+    fnorm = (torch.randn((h,), generator=g, device="cuda") * 0.1).to(torch.bfloat16)
+    r = np.random.Generator(np.random.PCG64(0))
+    pos = np.concatenate([b * 16384 + r.permutation(np.arange(16384 - nq * per, 16384)) for b in range(nreq)])
+    opt_pos = torch.as_tensor(pos.astype(np.int32), device="cuda")
+    opt_label = torch.as_tensor(r.integers(0, vocab, len(pos)).astype(np.int32), device="cuda")
+    q_off = torch.arange(0, len(pos) + 1, per, dtype=torch.int32, device="cuda")
+    ms = timed(lambda: K.readout(hidden, fnorm, table, opt_pos, opt_label, q_off, eps=1e-6, softcap=30.0))
+    nb = readout_bytes(h, len(pos), nreq * nq)
+    out["readout_27b_2048_options"] = {"ms": round(ms, 4), "gbps": round(nb / ms / 1e6, 1),
+                                       "frac_hbm_peak": round(nb / ms * 1e3 / PEAK_HBM, 4)}
     return out
+
+
+def decide_batch_throughput(weights, lengths: list[int], questions_per_request: int = QUESTIONS,
+                            reps: int = 3) -> dict:
+    """End-to-end `decide_batch` on text requests whose encoded lengths equal the forward's batch: the
+    byte tokenizer's encoding of the prompt and schema, packing, the host-to-device copy of ids and
+    descriptors, the forward, the device-to-host copy and the decode, timed on the host clock
+    (median of `reps` after one warm-up call). Every request asks the same `questions_per_request`
+    choice questions of 2-8 options."""
+    from deciax_amd.engine import DecisionEngine
+    from deciax_amd.schema import ByteTokenizer, encode
+
+    cfg = weights.config
+    tok = ByteTokenizer(cfg.vocab)
+    questions = {f"q{i}": {"type": "choice", "criteria": {f"o{j}": f"option {j} of field {i}"
+                                                          for j in range(2 + (i * 5) % 7)}}
+                 for i in range(questions_per_request)}
+    fixed = len(encode(tok, "", questions, vocab=cfg.vocab).ids)
+    r = np.random.Generator(np.random.PCG64(7))
+    letters = np.frombuffer(b"abcdefghijklmnopqrstuvwxyz ", np.uint8)
+    states = [bytes(r.choice(letters, max(1, n - fixed))).decode() for n in lengths]
+    engine = DecisionEngine(weights, tok, cfg.name)
+    engine.decide_batch(states, questions)
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        results = engine.decide_batch(states, questions)
+        times.append(time.perf_counter() - t0)
+    t = float(np.median(times))
+    tokens = sum(r_["usage"]["input_tokens"] for r_ in results)
+    return {"ms": round(t * 1e3, 2), "decisions_per_s": round(len(states) / t, 3),
+            "tokens_per_s": round(tokens / t, 1), "tokens": tokens, "requests": len(states),
+            "questions_per_request": questions_per_request,
+            "scope": "encode + pack + host-to-device + forward + device-to-host + decode, host clock, median of "
+                     f"{reps}"}
 
 
 def main() -> None:
@@ -302,6 +395,9 @@ def main() -> None:
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-configs", action="store_true", help="skip the single-kernel configurations")
+    ap.add_argument("--no-e2e", action="store_true", help="skip the end-to-end decide_batch timing")
+    ap.add_argument("--configs-only", action="store_true",
+                    help="run only the single-kernel configurations (for counter profiles) and print them")
     ap.add_argument("--model", choices=("gemma2-9b", "gemma2-27b"), default="gemma2-9b")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -314,6 +410,9 @@ def main() -> None:
     from deciax_amd import gemma
     from deciax_amd import kernels as K
 
+    if args.configs_only:
+        print(json.dumps({"kernel_configs": config_kernels()}))
+        return
     cfg = gemma.CONFIGS[args.model]
     t0 = time.time()
     weights = gemma.random_weights(cfg, seed=args.seed)
@@ -348,7 +447,8 @@ def main() -> None:
 
     kern = timer.summary()
     work = algorithmic_work(cfg, lengths)
-    nbytes = algorithmic_bytes(cfg, lengths)
+    n_options = sum(len(q) for req in options for q in req)
+    nbytes = algorithmic_bytes(cfg, lengths, n_options, n_questions)
     total_flops = tokens * cfg.linear_flops_per_token() + cfg.attention_flops(lengths)
     per_kernel = {}
     for name, s in sorted(kern.items(), key=lambda kv: -kv[1]["total_ms"]):
@@ -375,6 +475,11 @@ def main() -> None:
     }
     attn_ms = sum(kern[k]["total_ms"] for k in kern if k.startswith("attention")) / args.steps
     attn_flops = cfg.attention_flops(lengths)
+
+    e2e = None
+    if not args.no_e2e:
+        print("# end-to-end decide_batch", file=sys.stderr, flush=True)
+        e2e = decide_batch_throughput(weights, lengths)
 
     configs = None
     if not args.no_configs:
@@ -416,6 +521,7 @@ def main() -> None:
                       "frac_bf16_peak": round(attn_flops / (attn_ms * 1e-3) / PEAK_BF16, 4),
                       "ms_per_step": round(attn_ms, 2)},
         "kernels": per_kernel,
+        "decide_batch": e2e,
         "kernel_configs": configs,
         "roofline": roofline,
         "cpu_baseline": cpu,

@@ -237,59 +237,77 @@ pack_gate_up_kernel(const uint16_t *__restrict__ gate, const uint16_t *__restric
 
 // One workgroup per question; each wave scores options in turn, then the
 // workgroup takes the softmax over the question's options.
+// Readout: one workgroup per question, RO_WAVES waves, one option per wave at a time. Each wave requests
+// its option's hidden row and label row together, so an option costs one memory round trip (the norm
+// weights, shared by every option, come from L2); the products and the summation order are those of
+// row_scale.
+constexpr int RO_WAVES = 8;
+constexpr int RO_MAX_LDS = 512;  // the most options one request may hold
+
 template <int MAXC>
-__global__ void __launch_bounds__(THREADS)
+__global__ void __launch_bounds__(64 * RO_WAVES)
 readout_kernel(const uint16_t *__restrict__ hidden, const uint16_t *__restrict__ norm_w,
                const uint16_t *__restrict__ table, const int32_t *__restrict__ opt_pos,
                const int32_t *__restrict__ opt_label, const int32_t *__restrict__ q_off, long hidden_rows, int d,
                long ld_hidden,
                long vocab, float eps, float softcap, float *__restrict__ logits, float *__restrict__ probs) {
-  __shared__ float red[ROWS_PER_BLOCK];
+  __shared__ float red[RO_WAVES];
+  __shared__ float zs[RO_MAX_LDS];  // the question's logits, when it has at most RO_MAX_LDS options
   const int q = blockIdx.x;
   const int o0 = q_off[q], o1 = q_off[q + 1];
+  const bool in_lds = o1 - o0 <= RO_MAX_LDS;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int nch = d / 8;
-  for (int o = o0 + wave; o < o1; o += ROWS_PER_BLOCK) {
-    Row<MAXC> xr, gr;
+  for (int o = o0 + wave; o < o1; o += RO_WAVES) {
+    Row<MAXC> xr, er;
     const long prow = min(max((long)opt_pos[o], 0L), hidden_rows - 1);
-    load_row(xr, hidden + prow * ld_hidden, nch, lane);
-    const float inv = rms_inv(row_sumsq(xr, nch, lane), d, eps);
-    row_scale(gr, xr, norm_w, inv, nch, lane);
     const long lab = min(max((long)opt_label[o], 0L), vocab - 1);
-    const uint16_t *e = table + lab * d;
+    load_row(xr, hidden + prow * ld_hidden, nch, lane);
+    load_row(er, table + lab * d, nch, lane);
+    const float inv = rms_inv(row_sumsq(xr, nch, lane), d, eps);
     float dot = 0.f;
 #pragma unroll
     for (int i = 0; i < MAXC; ++i) {
       const int c = lane + 64 * i;
       if (c < nch) {
-        const u32x4 ec = *reinterpret_cast<const u32x4 *>(e + c * 8);
+        const u32x4 wc = *reinterpret_cast<const u32x4 *>(norm_w + c * 8);  // shared by every option: an L2 hit
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          dot = fmaf(lo_bf(gr.c[i][j]), lo_bf(ec[j]), dot);
-          dot = fmaf(hi_bf(gr.c[i][j]), hi_bf(ec[j]), dot);
+          const uint32_t g = pack_bf2((lo_bf(xr.c[i][j]) * inv) * (1.f + lo_bf(wc[j])),
+                                      (hi_bf(xr.c[i][j]) * inv) * (1.f + hi_bf(wc[j])));
+          dot = fmaf(lo_bf(g), lo_bf(er.c[i][j]), dot);
+          dot = fmaf(hi_bf(g), hi_bf(er.c[i][j]), dot);
         }
       }
     }
     dot = wave_sum(dot);
     const float z = softcap > 0.f ? softcap * tanhf(dot / softcap) : dot;
-    if (lane == 0) logits[o] = z;
+    if (lane == 0) {
+      logits[o] = z;
+      if (in_lds) zs[o - o0] = z;
+    }
   }
   __threadfence_block();
   __syncthreads();
+  auto logit = [&](int o) { return in_lds ? zs[o - o0] : logits[o]; };
   float m = -INFINITY;
-  for (int o = o0 + (int)threadIdx.x; o < o1; o += THREADS) m = fmaxf(m, logits[o]);
+  for (int o = o0 + (int)threadIdx.x; o < o1; o += 64 * RO_WAVES) m = fmaxf(m, logit(o));
   m = wave_max(m);
   if (lane == 0) red[wave] = m;
   __syncthreads();
-  m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  m = red[0];
+#pragma unroll
+  for (int w = 1; w < RO_WAVES; ++w) m = fmaxf(m, red[w]);
   __syncthreads();
   float s = 0.f;
-  for (int o = o0 + (int)threadIdx.x; o < o1; o += THREADS) s += expf(logits[o] - m);
+  for (int o = o0 + (int)threadIdx.x; o < o1; o += 64 * RO_WAVES) s += expf(logit(o) - m);
   s = wave_sum(s);
   if (lane == 0) red[wave] = s;
   __syncthreads();
-  s = red[0] + red[1] + red[2] + red[3];
-  for (int o = o0 + (int)threadIdx.x; o < o1; o += THREADS) probs[o] = expf(logits[o] - m) / s;
+  s = 0.f;
+#pragma unroll
+  for (int w = 0; w < RO_WAVES; ++w) s += red[w];
+  for (int o = o0 + (int)threadIdx.x; o < o1; o += 64 * RO_WAVES) probs[o] = expf(logit(o) - m) / s;
 }
 
 template <template <int> class F, typename... Args>
@@ -349,8 +367,8 @@ struct ReadoutRun {
   static hipError_t run(const uint16_t *hidden, const uint16_t *nw, const uint16_t *table, const int32_t *pos,
                         const int32_t *lab, const int32_t *q_off, int nq, long hrows, int d, long ldh, long vocab,
                         float eps, float softcap, float *logits, float *probs, hipStream_t s) {
-    readout_kernel<MAXC><<<dim3(nq), dim3(THREADS), 0, s>>>(hidden, nw, table, pos, lab, q_off, hrows, d, ldh, vocab,
-                                                            eps, softcap, logits, probs);
+    readout_kernel<MAXC><<<dim3(nq), dim3(64 * RO_WAVES), 0, s>>>(hidden, nw, table, pos, lab, q_off, hrows, d, ldh,
+                                                                  vocab, eps, softcap, logits, probs);
     return hipGetLastError();
   }
 };

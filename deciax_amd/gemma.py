@@ -299,6 +299,7 @@ class PackedBatch:
     # (seq_start, seq_len, vt_start) listed longest request first: the attention kernel launches
     # sequences in descriptor order, so the heaviest work starts first (outputs do not depend on it)
     by_length: tuple[torch.Tensor, torch.Tensor, torch.Tensor] | None = None
+    q_offsets_host: tuple[int, ...] = ()  # q_offsets on the host, for validation without a device read
 
     @property
     def rows(self) -> int:
@@ -341,7 +342,7 @@ def pack_batch(token_ids: Sequence[Sequence[int]], options: Sequence[Sequence[Se
     by_length = (i32(starts[order]), i32(np.asarray(lengths)[order]), i32(vt_start[order]))
     return PackedBatch(lengths, i32(ids), i32(positions), i32(starts), i32(lengths), i32(vt_start),
                        int(sum(padded)), i32(vt_col), i32(opt_pos), i32(opt_label), i32(q_off), qpr, opq,
-                       by_length)
+                       by_length, tuple(q_off))
 
 
 class Workspace:
@@ -413,4 +414,4 @@ def forward(w: DecisionWeights, batch: PackedBatch, ws: Workspace | None = None,
         if on_layer is not None:
             on_layer(i + 1, x)
     return K.readout(x, w.final_norm, w.embed, batch.opt_pos, batch.opt_label, batch.q_offsets, eps=c.eps,
-                     softcap=c.final_softcap)
+                     softcap=c.final_softcap, q_offsets_host=batch.q_offsets_host or None)

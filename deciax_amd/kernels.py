@@ -518,9 +518,11 @@ def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, key_mask: torch
 
 
 def readout(hidden: torch.Tensor, norm_w: torch.Tensor, table: torch.Tensor, opt_pos: torch.Tensor,
-            opt_label: torch.Tensor, q_offsets: torch.Tensor, *, eps: float,
-            softcap: float = 0.0) -> tuple[torch.Tensor, torch.Tensor]:
-    """Option logits and per-question probabilities (see dx_readout)."""
+            opt_label: torch.Tensor, q_offsets: torch.Tensor, *, eps: float, softcap: float = 0.0,
+            q_offsets_host: Sequence[int] | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """Option logits and per-question probabilities (see dx_readout). `q_offsets` is validated on a
+    host copy: pass `q_offsets_host` (the same values) to avoid reading the device tensor back, which
+    would synchronise the stream."""
     _need(hidden, "hidden", BF16, 2)
     _need(norm_w, "norm_w", BF16, 1)
     _need(table, "table", BF16, 2)
@@ -534,7 +536,9 @@ def readout(hidden: torch.Tensor, norm_w: torch.Tensor, table: torch.Tensor, opt
         raise ValueError(f"readout: norm_w and table rows must have {d} entries")
     if q_offsets.shape[0] < 1:
         raise ValueError("readout: q_offsets needs at least one entry")
-    offs = q_offsets.cpu()
+    offs = torch.as_tensor(q_offsets_host if q_offsets_host is not None else q_offsets.cpu())
+    if offs.shape != q_offsets.shape:
+        raise ValueError("readout: q_offsets_host must hold the values of q_offsets")
     if int(offs[0]) != 0 or int(offs[-1]) != nopt or bool((offs[1:] < offs[:-1]).any()):
         raise ValueError("readout: q_offsets must rise monotonically from 0 to the number of options")
     logits = torch.empty(nopt, dtype=F32, device=hidden.device)
