@@ -112,6 +112,8 @@ class KernelTimer:
             return "o_proj"
 
         wrap("linear", linear_label)
+        wrap("linear_residual_norm",
+             lambda a, k: "down_proj+norm" if a[1].shape[1] == config.intermediate else "o_proj+norm")
         wrap("gated_linear", lambda a, k: "gate_up_proj")
         wrap("attention_vt", lambda a, k: "attention_sliding" if k.get("window", 0) else "attention_global")
         wrap("add_rmsnorm", lambda a, k: "add_rmsnorm")
@@ -143,6 +145,8 @@ def algorithmic_work(cfg, lengths: list[int]) -> dict[str, float]:
         "o_proj": 2.0 * t * hq * d * h,
         "gate_up_proj": 2.0 * t * h * 2 * cfg.intermediate,
         "down_proj": 2.0 * t * cfg.intermediate * h,
+        "o_proj+norm": 2.0 * t * hq * d * h,               # the GEMM's FLOPs; the fused residual norm adds bytes
+        "down_proj+norm": 2.0 * t * cfg.intermediate * h,
         "attention_sliding": float(one.attention_flops(lengths)),
         "attention_global": float(replace(one, window=0).attention_flops(lengths)),
     }

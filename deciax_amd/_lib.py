@@ -64,6 +64,11 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
         [_p, _p, _p, _p, _p, _p, _p, _p, c_int64, c_int64, c_int32, c_int32, c_int32, c_int64, c_int64, c_int64,
          c_int32, _p],
     ),
+    "dx_linear_residual_norm": (
+        c_int,
+        [_p, _p, _p, _p, _p, _p, _p, _p, c_int64, c_int64, c_int64, c_int64, c_int64, c_float, _p],
+    ),
+    "dx_linear_residual_norm_counters": (c_int64, [c_int64]),
     "dx_pack_gate_up": (c_int, [_p, _p, _p, c_int64, c_int64, _p]),
     "dx_norm_project": (
         c_int, [_p, _p, _p, _p, _p, c_int64, c_int64, c_int64, c_float, _p, c_int64, _p]),

@@ -376,6 +376,36 @@ int dx_pack_gate_up(const void *gate, const void *up, void *packed, int64_t f, i
                       "pack_gate_up launch");
 }
 
+int64_t dx_linear_residual_norm_counters(int64_t m) { return m > 0 ? dx_gemm_norm_row_blocks(m) : 0; }
+
+int dx_linear_residual_norm(const void *a, const void *w, void *y, void *x, const void *post_w, const void *next_w,
+                            void *h, int32_t *counters, int64_t m, int64_t d, int64_t k, int64_t lda, int64_t ldw,
+                            float eps, void *stream) {
+  REQUIRE(a && w && y && x && post_w && counters, "linear_residual_norm: null pointer argument");
+  REQUIRE((h == nullptr) == (next_w == nullptr), "linear_residual_norm: h and next_w must both be set or both be null");
+  REQUIRE(m >= 0 && d > 0 && k > 0, "linear_residual_norm: bad sizes");
+  SUPPORTED(d % 256 == 0 && d <= 6144, "linear_residual_norm: d=%ld must be a multiple of 256 and <= 6144", (long)d);
+  SUPPORTED(k % 64 == 0, "linear_residual_norm: k=%ld must be a multiple of 64", (long)k);
+  REQUIRE(lda >= k && ldw >= k && lda % 8 == 0 && ldw % 8 == 0,
+          "linear_residual_norm: leading dimensions must cover the row and be multiples of 8");
+  SUPPORTED(lda <= DX_MAX_LD && ldw <= DX_MAX_LD && d <= DX_MAX_LD,
+            "linear_residual_norm: leading dimensions above %d", DX_MAX_LD);
+  REQUIRE(aligned16(a) && aligned16(w) && aligned16(y) && aligned16(x) && aligned16(post_w) &&
+              (!h || (aligned16(h) && aligned16(next_w))) && (reinterpret_cast<uintptr_t>(counters) & 3) == 0,
+          "linear_residual_norm: pointers must be 16-byte aligned (counters 4-byte)");
+  if (m == 0) return DX_OK;
+  NormEpilogue ne;
+  ne.x = static_cast<uint16_t *>(x);
+  ne.post_w = static_cast<const uint16_t *>(post_w);
+  ne.next_w = static_cast<const uint16_t *>(next_w);
+  ne.h = static_cast<uint16_t *>(h);
+  ne.counters = counters;
+  ne.eps = eps;
+  return check_launch(dx_gemm_norm(static_cast<const uint16_t *>(a), static_cast<const uint16_t *>(w),
+                                   static_cast<uint16_t *>(y), m, d, k, lda, ldw, ne, as_stream(stream)),
+                      "linear_residual_norm launch");
+}
+
 int64_t dx_norm_project_workspace(int64_t rows, int64_t d) { return align_up(rows * d * 2, 256); }
 
 int dx_norm_project(const void *x, const void *norm_w, const uint8_t *row_mask, const void *w, void *y, int64_t rows,

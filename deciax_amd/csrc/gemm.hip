@@ -47,6 +47,7 @@
 // attention kernel stages (one column per token: vt_col[row]).
 #include "common.h"
 #include "kernels.h"
+#include "rownorm.h"
 
 namespace {
 
@@ -64,7 +65,7 @@ constexpr int BK = 64;
 constexpr int BN = 256;
 constexpr int THREADS = 256;
 
-enum { EPI_BF16 = 0, EPI_F32 = 1, EPI_GATED = 2, EPI_QKV = 3 };
+enum { EPI_BF16 = 0, EPI_F32 = 1, EPI_GATED = 2, EPI_QKV = 3, EPI_NORM = 4 };
 
 // Workgroups are dispatched round-robin over the 8 XCDs (each with its own
 // L2). Renumber so each XCD gets a contiguous run of logical tiles, then walk
@@ -99,10 +100,66 @@ DX_DEVICE __amdgpu_buffer_rsrc_t make_rsrc(const uint16_t *base, long bytes) {
   return __builtin_amdgcn_make_buffer_rsrc((void *)base, (short)0, (int)bytes, 0x00020000);
 }
 
+// After a workgroup's y tile has been stored (system-coherent), count its row block; the workgroup that
+// completes the block's num_n column tiles applies the residual update to the block's rows, one wave
+// per row (add_rmsnorm_row, the arithmetic of dx_add_rmsnorm), and resets the counter for the next
+// call. No workgroup waits for another, so the grid needs no co-residency.
+template <int BM>
+DX_DEVICE void norm_epilogue(const uint16_t *Y, int M, int N, long ldy, int m0, int tm, int num_n,
+                             const NormEpilogue &ne, int *flag) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this thread's y stores have reached memory
+  __syncthreads();  // ... every thread's; the staged tile in LDS is no longer read, so `flag` may reuse it
+  if (tid == 0)
+    *flag = __hip_atomic_fetch_add(ne.counters + tm, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM) == num_n - 1;
+  __syncthreads();
+  if (!*flag) return;
+  const int rows = min(BM, M - m0);
+  // Each wave takes RB rows at a time and requests all of their y and x before computing any, so a
+  // wave keeps RB rows of memory latency in flight instead of one.
+  constexpr int WAVES = THREADS / 64;
+  auto run = [&](auto maxc, auto next) __attribute__((always_inline)) {
+    constexpr int MC = decltype(maxc)::value;
+    constexpr bool NX = decltype(next)::value;
+    constexpr int RB = MC <= 8 ? 3 : 2;  // 2 RB MC 16-byte chunks of registers per lane
+    const int nch = N / 8;
+    for (int r0 = wave; r0 < rows; r0 += RB * WAVES) {
+      Row<MC> yr[RB], xr[RB];
+#pragma unroll
+      for (int b = 0; b < RB; ++b) {
+        const int r = r0 + b * WAVES;
+        if (r < rows) {
+          load_row_coherent(yr[b], Y + (long)(m0 + r) * ldy, nch, lane);
+          load_row(xr[b], ne.x + (long)(m0 + r) * N, nch, lane);
+        }
+      }
+#pragma unroll
+      for (int b = 0; b < RB; ++b) {
+        const int r = r0 + b * WAVES;
+        if (r < rows) {
+          const long row = m0 + r;
+          add_rmsnorm_regs<MC, NX>(yr[b], xr[b], ne.post_w, ne.x + row * N, ne.next_w,
+                                   NX ? ne.h + row * N : nullptr, N, ne.eps, lane);
+        }
+      }
+    }
+  };
+  // up to 8 chunks of 8 columns per lane (N <= 4096, the 9B width) or 12 (N <= 6144, the 27B width)
+  const bool wide = N > 64 * 8 * 8;
+  if (ne.next_w) {
+    if (wide) run(Int<12>(), Flag<true>());
+    else run(Int<8>(), Flag<true>());
+  } else {
+    if (wide) run(Int<12>(), Flag<false>());
+    else run(Int<8>(), Flag<false>());
+  }
+  if (tid == 0) __hip_atomic_store(ne.counters + tm, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
 template <int BM, int EPI, bool DTL>
 __global__ void __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(1, 1)))
 gemm_nt_kernel(const uint16_t *__restrict__ A, const uint16_t *__restrict__ B, void *__restrict__ C, int M, int N,
-               int K, long lda, long ldb, long ldc, int act, int group_m, QkvEpilogue qe) {
+               int K, long lda, long ldb, long ldc, int act, int group_m, QkvEpilogue qe, NormEpilogue ne) {
   constexpr int TM = BM / 64, TN = BN / 64;  // 32x32 blocks per wave along m, n
   constexpr int STAGE = (BM + BN) * BK;
   constexpr int AC = BM * BK / 8 / THREADS, BC = BN * BK / 8 / THREADS;  // 16-byte chunks per thread
@@ -472,7 +529,7 @@ gemm_nt_kernel(const uint16_t *__restrict__ A, const uint16_t *__restrict__ B, v
             smem[col * TP + row] = f2bf(acc[i][j][r]);
           }
       }
-    } else if constexpr (EPI == EPI_BF16 || EPI == EPI_QKV) {
+    } else if constexpr (EPI == EPI_BF16 || EPI == EPI_QKV || EPI == EPI_NORM) {
 #pragma unroll
       for (int i = 0; i < TM; ++i) {
         const int row = wm * (BM / 2) + i * 32 + lrow;
@@ -592,6 +649,18 @@ gemm_nt_kernel(const uint16_t *__restrict__ A, const uint16_t *__restrict__ B, v
             qe.vt[(long)(n0 + c - qe.qk_cols) * qe.vt_ld + col] = smem[row * OUT_PITCH + c];
         }
       }
+    } else if constexpr (EPI == EPI_NORM) {
+      // System-coherent stores (sc0 sc1: they reach memory, not only this XCD's L2): the row block's last
+      // workgroup reads the tile back within this kernel, possibly from another XCD.
+      constexpr int CPR = OUT_W / 8;
+      const __amdgpu_buffer_rsrc_t rc = make_rsrc(Cb + (long)m0 * ldc, (long)min(M - m0, BM) * ldc * 2);
+      for (int idx = tid; idx < BM * CPR; idx += THREADS) {
+        const int row = idx / CPR, c = idx % CPR;
+        if (m0 + row < M)
+          __builtin_amdgcn_raw_buffer_store_b128(*reinterpret_cast<const u32x4 *>(smem + row * OUT_PITCH + c * 8),
+                                                 rc, (int)((row * ldc + n0 + c * 8) * 2), 0, 17);
+      }
+      norm_epilogue<BM>(Cb, M, N, ldc, m0, tm, num_n, ne, reinterpret_cast<int *>(smem));
     } else {
       const int out_n0 = EPI == EPI_GATED ? n0 / 2 : n0;
       constexpr int CPR = OUT_W / 8;  // 16-byte chunks per row
@@ -607,7 +676,7 @@ gemm_nt_kernel(const uint16_t *__restrict__ A, const uint16_t *__restrict__ B, v
 
 template <int BM, int EPI>
 hipError_t launch(const uint16_t *A, const uint16_t *B, void *C, long M, long N, long K, long lda, long ldb,
-                  long ldc, int act, const QkvEpilogue &qe, hipStream_t s) {
+                  long ldc, int act, const QkvEpilogue &qe, const NormEpilogue &ne, hipStream_t s) {
   const long num_m = (M + BM - 1) / BM, num_n = N / BN;
   // 256-row tiles always take the direct-to-LDS ring: its A stages give long-K shapes the latency slack
   // (against the register-staged path: down K 14336 +3-8 % alone and -0.8 % step time in the 9B
@@ -620,18 +689,19 @@ hipError_t launch(const uint16_t *A, const uint16_t *B, void *C, long M, long N,
   // re-read it once per 4 column tiles (9B down, K 14336: +4%; K 36864: 0%); 4 for the plain bf16 /
   // fp32 epilogues (o at 9B and 27B: +1.5-2%); 8 for the gated and q|k|v epilogues, where 4 measured
   // mixed (27B q|k|v -4.7%).
-  const int group_m = K >= 8192 ? 2 : (EPI == EPI_BF16 || EPI == EPI_F32) ? 4 : 8;
+  const int group_m = K >= 8192 ? 2 : (EPI == EPI_BF16 || EPI == EPI_F32 || EPI == EPI_NORM) ? 4 : 8;
   kern<<<dim3((unsigned)(num_m * num_n)), dim3(THREADS), 0, s>>>(A, B, C, (int)M, (int)N, (int)K, lda, ldb, ldc,
-                                                                 act, group_m, qe);
+                                                                 act, group_m, qe, ne);
   return hipGetLastError();
 }
 
 template <int EPI>
 hipError_t dispatch(const uint16_t *A, const uint16_t *B, void *C, long M, long N, long K, long lda, long ldb,
-                    long ldc, int act, hipStream_t s, const QkvEpilogue &qe = QkvEpilogue{}) {
+                    long ldc, int act, hipStream_t s, const QkvEpilogue &qe = QkvEpilogue{},
+                    const NormEpilogue &ne = NormEpilogue{}) {
   // Small M: halve the row tile so more workgroups exist.
-  if (M <= 1024) return launch<128, EPI>(A, B, C, M, N, K, lda, ldb, ldc, act, qe, s);
-  return launch<256, EPI>(A, B, C, M, N, K, lda, ldb, ldc, act, qe, s);
+  if (M <= 1024) return launch<128, EPI>(A, B, C, M, N, K, lda, ldb, ldc, act, qe, ne, s);
+  return launch<256, EPI>(A, B, C, M, N, K, lda, ldb, ldc, act, qe, ne, s);
 }
 
 }  // namespace
@@ -655,3 +725,10 @@ hipError_t dx_gemm_qkv(const uint16_t *A, const uint16_t *B, uint16_t *QK, long 
                        long ld_qk, const QkvEpilogue &qe, hipStream_t s) {
   return dispatch<EPI_QKV>(A, B, QK, M, N, K, lda, ldb, ld_qk, 0, s, qe);
 }
+
+hipError_t dx_gemm_norm(const uint16_t *A, const uint16_t *B, uint16_t *C, long M, long N, long K, long lda,
+                        long ldb, const NormEpilogue &ne, hipStream_t s) {
+  return dispatch<EPI_NORM>(A, B, C, M, N, K, lda, ldb, N, 0, s, QkvEpilogue{}, ne);
+}
+
+long dx_gemm_norm_row_blocks(long M) { return M <= 1024 ? (M + 127) / 128 : (M + 255) / 256; }

@@ -29,6 +29,23 @@ struct QkvEpilogue {
 };
 hipError_t dx_gemm_qkv(const uint16_t *A, const uint16_t *B, uint16_t *QK, long M, long N, long K, long lda, long ldb,
                        long ld_qk, const QkvEpilogue &qe, hipStream_t s);
+
+// Residual-norm epilogue of an output projection whose N is the hidden width d: y = bf16(A @ B^T) is
+// stored (system-coherent) to C, and the last workgroup to finish a row block's column tiles applies
+//   x = bf16(x + bf16(rms(y) (1 + post_w)));  if next_w: h = bf16(rms(x) (1 + next_w))
+// to the block's rows (x, h: [M, N] contiguous). counters: one int per row block of the launch's tile
+// height, zero before the call and left zero after it.
+struct NormEpilogue {
+  uint16_t *x = nullptr;
+  const uint16_t *post_w = nullptr, *next_w = nullptr;
+  uint16_t *h = nullptr;
+  int *counters = nullptr;
+  float eps = 0.f;
+};
+hipError_t dx_gemm_norm(const uint16_t *A, const uint16_t *B, uint16_t *C, long M, long N, long K, long lda,
+                        long ldb, const NormEpilogue &ne, hipStream_t s);
+// Row blocks (counters) dx_gemm_norm uses for M rows.
+long dx_gemm_norm_row_blocks(long M);
 hipError_t dx_vt_zero_tails_launch(uint16_t *vt, const int32_t *seq_len, const int32_t *vt_start, int num_seqs,
                                    int vt_rows, long vt_ld, hipStream_t s);
 

@@ -8,89 +8,12 @@
 //   v = x * rsqrt(mean(x^2) + eps);  v = v * (1 + w);  round to bf16.
 #include "common.h"
 #include "kernels.h"
+#include "rownorm.h"
 
 namespace {
 
 constexpr int THREADS = 256;
 constexpr int ROWS_PER_BLOCK = THREADS / 64;
-
-template <int MAXC>
-struct Row {
-  u32x4 c[MAXC];
-};
-
-template <int MAXC>
-DX_DEVICE void load_row(Row<MAXC> &r, const uint16_t *p, int nch, int lane) {
-#pragma unroll
-  for (int i = 0; i < MAXC; ++i) {
-    const int c = lane + 64 * i;
-    if (c < nch) r.c[i] = *reinterpret_cast<const u32x4 *>(p + c * 8);
-  }
-}
-
-template <int MAXC>
-DX_DEVICE void store_row(const Row<MAXC> &r, uint16_t *p, int nch, int lane) {
-#pragma unroll
-  for (int i = 0; i < MAXC; ++i) {
-    const int c = lane + 64 * i;
-    if (c < nch) *reinterpret_cast<u32x4 *>(p + c * 8) = r.c[i];
-  }
-}
-
-template <int MAXC>
-DX_DEVICE float row_sumsq(const Row<MAXC> &r, int nch, int lane) {
-  float ss = 0.f;
-#pragma unroll
-  for (int i = 0; i < MAXC; ++i) {
-    const int c = lane + 64 * i;
-    if (c < nch) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float a = lo_bf(r.c[i][j]), b = hi_bf(r.c[i][j]);
-        ss = fmaf(a, a, ss);
-        ss = fmaf(b, b, ss);
-      }
-    }
-  }
-  return wave_sum(ss);
-}
-
-// out = bf16((x * inv) * (1 + w)) with w already loaded (the same products as row_scale).
-template <int MAXC>
-DX_DEVICE void row_scale_w(Row<MAXC> &out, const Row<MAXC> &x, const Row<MAXC> &w, float inv, int nch, int lane) {
-#pragma unroll
-  for (int i = 0; i < MAXC; ++i) {
-    const int c = lane + 64 * i;
-    if (c < nch) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float a = (lo_bf(x.c[i][j]) * inv) * (1.f + lo_bf(w.c[i][j]));
-        const float b = (hi_bf(x.c[i][j]) * inv) * (1.f + hi_bf(w.c[i][j]));
-        out.c[i][j] = pack_bf2(a, b);
-      }
-    }
-  }
-}
-
-// out = bf16((x * inv) * (1 + w)), elementwise over the row.
-template <int MAXC>
-DX_DEVICE void row_scale(Row<MAXC> &out, const Row<MAXC> &x, const uint16_t *w, float inv, int nch, int lane) {
-#pragma unroll
-  for (int i = 0; i < MAXC; ++i) {
-    const int c = lane + 64 * i;
-    if (c < nch) {
-      const u32x4 wc = *reinterpret_cast<const u32x4 *>(w + c * 8);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float a = (lo_bf(x.c[i][j]) * inv) * (1.f + lo_bf(wc[j]));
-        const float b = (hi_bf(x.c[i][j]) * inv) * (1.f + hi_bf(wc[j]));
-        out.c[i][j] = pack_bf2(a, b);
-      }
-    }
-  }
-}
-
-DX_DEVICE float rms_inv(float ss, int d, float eps) { return rsqrtf(ss / (float)d + eps); }
 
 template <int MAXC>
 __global__ void __launch_bounds__(THREADS)
@@ -118,42 +41,7 @@ add_rmsnorm_kernel(const uint16_t *__restrict__ y, const uint16_t *__restrict__ 
   const long row = (long)blockIdx.x * ROWS_PER_BLOCK + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   if (row >= rows) return;
-  const int nch = d / 8;
-  // Rows of up to 8 chunks per lane (H <= 4096) request the norm weights with the rows (the next
-  // norm's once the first is used), so their latency hides behind the row loads and the sums
-  // (H 3584: -3.8%). Longer rows read them where used: a third register row costs them occupancy
-  // (H 4608: +14%).
-  constexpr bool PREFETCH = MAXC <= 8;
-  Row<MAXC> yr, xr, wr;
-  load_row(yr, y + row * d, nch, lane);
-  load_row(xr, x + row * d, nch, lane);
-  if constexpr (PREFETCH && POST) load_row(wr, post_w, nch, lane);
-  else if constexpr (PREFETCH && NEXT) load_row(wr, next_w, nch, lane);
-  if constexpr (POST) {
-    const float inv = rms_inv(row_sumsq(yr, nch, lane), d, eps);
-    if constexpr (PREFETCH) {
-      row_scale_w(yr, yr, wr, inv, nch, lane);
-      if constexpr (NEXT) load_row(wr, next_w, nch, lane);
-    } else {
-      row_scale(yr, yr, post_w, inv, nch, lane);
-    }
-  }
-#pragma unroll
-  for (int i = 0; i < MAXC; ++i) {
-    const int c = lane + 64 * i;
-    if (c < nch) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        xr.c[i][j] = pack_bf2(lo_bf(xr.c[i][j]) + lo_bf(yr.c[i][j]), hi_bf(xr.c[i][j]) + hi_bf(yr.c[i][j]));
-    }
-  }
-  store_row(xr, x + row * d, nch, lane);
-  if constexpr (NEXT) {
-    const float inv = rms_inv(row_sumsq(xr, nch, lane), d, eps);
-    if constexpr (PREFETCH) row_scale_w(yr, xr, wr, inv, nch, lane);
-    else row_scale(yr, xr, next_w, inv, nch, lane);
-    store_row(yr, h + row * d, nch, lane);
-  }
+  add_rmsnorm_row<MAXC, POST, NEXT, false>(y + row * d, post_w, x + row * d, next_w, h + row * d, d, eps, lane);
 }
 
 template <int MAXC, bool NORM>

@@ -11,11 +11,11 @@ call into the gfx950 kernels:
         in the epilogue, V written transposed (V^T)
       causal GQA flash attention, softcap 50,          dx_attn_prefill_vt
         sliding window 4096 on even layers
-      y = att @ Wo^T                                   dx_linear
-      x += post_attn_norm(y); h = pre_ffn_norm(x)      dx_add_rmsnorm
+      y = att @ Wo^T; x += post_attn_norm(y);          dx_linear_residual_norm
+        h = pre_ffn_norm(x)
       a = gelu_tanh(h Wg^T) * (h Wu^T)                 dx_gated_linear
-      y = a @ Wd^T                                     dx_linear
-      x += post_ffn_norm(y); h = next input_norm(x)    dx_add_rmsnorm
+      y = a @ Wd^T; x += post_ffn_norm(y);             dx_linear_residual_norm
+        h = next input_norm(x)
     final norm + gather + label dot + softcap 30 +
       per-question softmax                             dx_readout
 
@@ -358,6 +358,7 @@ class Workspace:
         self.att = torch.empty((rows, c.heads * c.head_dim), dtype=BF16, device=device)
         self.act = torch.empty((rows, c.intermediate), dtype=BF16, device=device)
         self.vt = torch.empty((c.kv_heads * c.head_dim, max(vt_ld, 64)), dtype=BF16, device=device)
+        self.counters = K.residual_norm_counters(rows, device)  # row blocks of the fused o / down epilogues
 
     def fits(self, rows: int, vt_ld: int) -> bool:
         return rows <= self.rows and vt_ld <= self.vt.shape[1]
@@ -366,6 +367,12 @@ class Workspace:
 def embed_scale(hidden: int) -> float:
     """sqrt(H) rounded to bf16, the Gemma-2 normaliser (TF/models/gemma2/modeling_gemma2.py:338-349)."""
     return float(torch.tensor(math.sqrt(hidden), dtype=torch.float32).to(BF16).float())
+
+
+# True folds each post-norm residual update into the o / down GEMM's epilogue
+# (dx_linear_residual_norm): bit-identical to the separate GEMM + dx_add_rmsnorm, but slower at
+# prefill sizes, since one workgroup per 256-row block normalises its rows after the main loop.
+FUSED_NORM = False
 
 
 def layer_forward(w: DecisionWeights, i: int, batch: PackedBatch, ws: Workspace) -> None:
@@ -383,12 +390,19 @@ def layer_forward(w: DecisionWeights, i: int, batch: PackedBatch, ws: Workspace)
     K.attention_vt(qkv[:, :qd], qkv[:, qd:qd + kd], vt, seq_start, seq_len, vt_start, batch.max_len,
                    num_q_heads=c.heads, num_kv_heads=c.kv_heads, head_dim=c.head_dim, scale=c.query_scale,
                    softcap=c.attn_softcap, window=c.window if c.sliding(i) else 0, causal=True, out=att)
-    K.linear(att, lw.o, out=y)
-    K.add_rmsnorm(y, x, eps=c.eps, post_w=lw.post_attn_norm, next_w=lw.pre_ffn_norm, h=h)
-    K.gated_linear(h, lw.gate_up, c.activation, out=act)
-    K.linear(act, lw.down, out=y)
     nxt = w.layers[i + 1].input_norm if i + 1 < len(w.layers) else None
-    K.add_rmsnorm(y, x, eps=c.eps, post_w=lw.post_ffn_norm, next_w=nxt, h=h if nxt is not None else None)
+    if FUSED_NORM:
+        K.linear_residual_norm(att, lw.o, y, x, lw.post_attn_norm, eps=c.eps, counters=ws.counters,
+                               next_w=lw.pre_ffn_norm, h=h)
+        K.gated_linear(h, lw.gate_up, c.activation, out=act)
+        K.linear_residual_norm(act, lw.down, y, x, lw.post_ffn_norm, eps=c.eps, counters=ws.counters,
+                               next_w=nxt, h=h if nxt is not None else None)
+    else:
+        K.linear(att, lw.o, out=y)
+        K.add_rmsnorm(y, x, eps=c.eps, post_w=lw.post_attn_norm, next_w=lw.pre_ffn_norm, h=h)
+        K.gated_linear(h, lw.gate_up, c.activation, out=act)
+        K.linear(act, lw.down, out=y)
+        K.add_rmsnorm(y, x, eps=c.eps, post_w=lw.post_ffn_norm, next_w=nxt, h=h if nxt is not None else None)
 
 
 def forward(w: DecisionWeights, batch: PackedBatch, ws: Workspace | None = None, layers: int | None = None,

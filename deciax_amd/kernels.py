@@ -119,6 +119,48 @@ def qkv_rope(x: torch.Tensor, w_qkv: torch.Tensor, qk: torch.Tensor, vt: torch.T
     return qk
 
 
+def residual_norm_counters(rows: int, device: torch.device | str) -> torch.Tensor:
+    """Zeroed row-block counters for `linear_residual_norm` on up to `rows` rows (each completed call
+    leaves them zero, so one array serves a whole forward)."""
+    n = max(int(_lib.lib().dx_linear_residual_norm_counters(max(rows, 1))),
+            int(_lib.lib().dx_linear_residual_norm_counters(min(max(rows, 1), 1024))))
+    return torch.zeros(n, dtype=torch.int32, device=device)
+
+
+def linear_residual_norm(a: torch.Tensor, w: torch.Tensor, y: torch.Tensor, x: torch.Tensor, post_w: torch.Tensor,
+                         *, eps: float, counters: torch.Tensor, next_w: torch.Tensor | None = None,
+                         h: torch.Tensor | None = None) -> torch.Tensor | None:
+    """y = a @ w.T (bf16), then in place x = bf16(x + bf16(rms(y)(1 + post_w))) and, with `next_w`,
+    h = bf16(rms(x)(1 + next_w)): `linear` followed by `add_rmsnorm`, bit-identically, in one kernel
+    (dx_linear_residual_norm). y is scratch; `counters` comes from `residual_norm_counters`."""
+    for t, n in ((a, "a"), (w, "w"), (y, "y"), (x, "x")):
+        _need(t, n, BF16, 2)
+    m, k = a.shape
+    d = w.shape[0]
+    if w.shape[1] != k:
+        raise ValueError(f"linear_residual_norm: a {tuple(a.shape)} and w {tuple(w.shape)} disagree on k")
+    for t, n in ((y, "y"), (x, "x")):
+        if tuple(t.shape) != (m, d) or not t.is_contiguous():
+            raise ValueError(f"linear_residual_norm: {n} must be a contiguous [{m}, {d}] tensor")
+    for t, n in ((post_w, "post_w"), (next_w, "next_w")):
+        if t is not None:
+            _need(t, n, BF16, 1)
+            if t.shape[0] != d or not t.is_contiguous():
+                raise ValueError(f"linear_residual_norm: {n} must be a contiguous [{d}] tensor")
+    if (h is None) != (next_w is None):
+        raise ValueError("linear_residual_norm: h and next_w go together")
+    if h is not None:
+        _need(h, "h", BF16, 2)
+        if tuple(h.shape) != (m, d) or not h.is_contiguous():
+            raise ValueError(f"linear_residual_norm: h must be a contiguous [{m}, {d}] tensor")
+    _need(counters, "counters", torch.int32, 1)
+    if counters.shape[0] < _lib.lib().dx_linear_residual_norm_counters(m) or not counters.is_contiguous():
+        raise ValueError("linear_residual_norm: counters too short; use residual_norm_counters")
+    call("dx_linear_residual_norm", _ptr(a), _ptr(w), _ptr(y), _ptr(x), _ptr(post_w), _ptr(next_w), _ptr(h),
+         _ptr(counters), m, d, k, _rows(a, "a"), _rows(w, "w"), float(eps), _stream())
+    return h
+
+
 def pack_gate_up(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
     """[f, k] gate and up weights -> the [2f, k] packed layout of `gated_linear`
     (the role of `pack`, src/deciax/kernels/swiglu.py:45-51)."""

@@ -260,6 +260,29 @@ int dx_mlp(const void *x, const void *norm_w, const void *gate_up,
 
 int64_t dx_mlp_workspace(int64_t rows, int64_t d, int64_t f);
 
+/* Output projection with the sandwich-norm residual update fused behind it:
+ *   y = bf16(a @ w^T)                            ([m, d], d = hidden width)
+ *   x = bf16(x + bf16(rms(y) * (1 + post_w)))
+ *   if next_w: h = bf16(rms(x) * (1 + next_w))
+ * with x, h [m, d] contiguous and y a caller-provided [m, d] scratch (its
+ * contents are undefined afterwards). The results are bit-identical to
+ * dx_linear followed by dx_add_rmsnorm. Replaces the o / down projection plus
+ * the fp32-partial -> bf16 residual step of src/deciax/models/qwen3_5/pallas.py:64-70
+ * (post-norm and residual of the Gemma-2 sandwich layer,
+ * TF/models/gemma2/modeling_gemma2.py:313-333), in the spirit of the fused
+ * o-projection + residual + norm of src/deciax/kernels/fused.py:216-247.
+ * The last workgroup to finish a row block's column tiles applies the update to
+ * the block's rows; `counters` holds dx_linear_residual_norm_counters(m) int32
+ * values that must be zero before the first call and are left zero by every
+ * completed call (calls sharing one counter array must not overlap). Requires
+ * d % 256 == 0 and d <= 6144, k % 64 == 0, 16-byte aligned operands. */
+int dx_linear_residual_norm(const void *a, const void *w, void *y, void *x,
+                            const void *post_w, const void *next_w, void *h,
+                            int32_t *counters, int64_t m, int64_t d, int64_t k,
+                            int64_t lda, int64_t ldw, float eps, void *stream);
+
+int64_t dx_linear_residual_norm_counters(int64_t m);
+
 /* ------------------------------------------------------------------------ */
 /* Norms, embedding, RoPE                                                    */
 /* ------------------------------------------------------------------------ */

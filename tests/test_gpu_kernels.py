@@ -667,3 +667,67 @@ def test_abi_rejects_bad_arguments() -> None:
     with pytest.raises(ValueError, match="one field index"):
         K.head_routing_f32(xf, xf[:2], i32([[0, 0]]), torch.ones((1, 4), dtype=torch.uint8, device="cuda"),
                            batch=1)
+
+
+@pytest.mark.parametrize("m,d,k,with_next", [
+    (333, 512, 256, True),          # 128-row tiles
+    (1025, 512, 1024, False),       # 256-row tiles, a 1-row last block, no next norm
+    (4173, 3584, 4096, True),       # the 9B o projection
+    (2100, 3584, 14336, True),      # the 9B down projection (long K)
+    (700, 4608, 4096, True),        # the 27B width, 128-row tiles
+    (1300, 4608, 36864, False),     # the 27B down projection, 256-row tiles
+])
+def test_linear_residual_norm_matches_unfused(m: int, d: int, k: int, with_next: bool) -> None:
+    """The fused o / down projection with the post-norm residual update is bit-identical to dx_linear
+    followed by dx_add_rmsnorm, leaves its row-block counters at zero, and gives the same result when
+    the counters are reused."""
+    import torch
+
+    from deciax_amd import kernels as K
+
+    say(f"linear_residual_norm m={m} d={d} k={k} next={with_next}")
+    g = torch.Generator(device="cuda").manual_seed(m + d + k)
+    a = torch.randn((m, k), generator=g, device="cuda").to(torch.bfloat16)
+    w = (torch.randn((d, k), generator=g, device="cuda") * 0.02).to(torch.bfloat16)
+    x0 = torch.randn((m, d), generator=g, device="cuda").to(torch.bfloat16)
+    post_w = (torch.randn((d,), generator=g, device="cuda") * 0.3).to(torch.bfloat16)
+    next_w = (torch.randn((d,), generator=g, device="cuda") * 0.3).to(torch.bfloat16) if with_next else None
+
+    y1 = K.linear(a, w)
+    x1 = x0.clone()
+    h1 = K.add_rmsnorm(y1, x1, eps=1e-6, post_w=post_w, next_w=next_w)
+    counters = K.residual_norm_counters(m, "cuda")
+    for _ in range(2):
+        x2, y2 = x0.clone(), torch.full_like(x0, float("nan"))
+        h2 = torch.full_like(x0, float("nan")) if with_next else None
+        K.linear_residual_norm(a, w, y2, x2, post_w, eps=1e-6, counters=counters, next_w=next_w, h=h2)
+        torch.cuda.synchronize()
+        assert torch.equal(y2, y1)
+        assert torch.equal(x2, x1)
+        if with_next:
+            assert torch.equal(h2, h1)
+        assert int(counters.abs().sum()) == 0
+
+
+def test_fused_residual_norm_forward_bit_identical() -> None:
+    """The 9B-shaped forward at the benchmark batch (16 requests, 70471 tokens, 42 layers): the same
+    logits and probabilities with the residual norm fused into the o / down epilogues and without."""
+    import bench
+    from deciax_amd import gemma
+
+    say("9b forward, fused vs unfused residual norm")
+    cfg = gemma.CONFIGS["gemma2-9b"]
+    lengths, ids, options = bench.synthetic_batch(cfg.vocab, seed=0)
+    w = gemma.random_weights(cfg, seed=0)
+    batch = gemma.pack_batch(ids, options)
+    ws = gemma.Workspace(cfg, batch.rows, batch.vt_ld, w.device)
+    out, default = {}, gemma.FUSED_NORM
+    try:
+        for fused in (True, False):
+            gemma.FUSED_NORM = fused
+            z, p = gemma.forward(w, batch, ws)
+            out[fused] = (z.cpu().numpy(), p.cpu().numpy())
+    finally:
+        gemma.FUSED_NORM = default
+    assert np.array_equal(out[True][0], out[False][0])
+    assert np.array_equal(out[True][1], out[False][1])
