@@ -106,8 +106,9 @@ def embed_scale(hidden: int, bf16: bool = True) -> float:
 
 def layer(x: np.ndarray, p: Mapping[str, np.ndarray], shape: Shape, index: int, seq_start: Sequence[int],
           seq_len: Sequence[int], positions: np.ndarray, cos: np.ndarray, sin: np.ndarray,
-          bf16: bool = True) -> np.ndarray:
-    """One sandwich layer over packed rows x [R, H]."""
+          bf16: bool = True, rounding: str = "flash") -> np.ndarray:
+    """One sandwich layer over packed rows x [R, H]; `rounding` is attention_seq's bf16 rounding
+    point of the attention weights."""
     s = shape
     h = rmsnorm(x, p["input_norm"], s.eps, bf16)
     rows = x.shape[0]
@@ -121,7 +122,7 @@ def layer(x: np.ndarray, p: Mapping[str, np.ndarray], shape: Shape, index: int, 
     for start, length in zip(seq_start, seq_len):
         sl = slice(start, start + length)
         att[sl] = attention_seq(q[sl], k[sl], v[sl], scale=s.query_scale, softcap_value=s.attn_softcap,
-                                window=window, causal=True, bf16=bf16)
+                                window=window, causal=True, bf16=bf16, rounding=rounding)
     y = linear(att.reshape(rows, -1), p["o"], bf16)
     x = maybe(x + rmsnorm(y, p["post_attn_norm"], s.eps, bf16), bf16)
     h = rmsnorm(x, p["pre_ffn_norm"], s.eps, bf16)

@@ -76,9 +76,13 @@ def _top2_gap(p: np.ndarray) -> float:
     return float(top[0] - top[1])
 
 
-def check_forward(name: str, weights, batch) -> ForwardParity:
+def check_forward(name: str, weights, batch, rounding: str = "flash") -> ForwardParity:
     """Run the HIP forward on `batch` (weights built with keep_unpacked=True) and check it against
-    the oracle as the module docstring describes. Returns the measured numbers."""
+    the oracle as the module docstring describes. Returns the measured numbers.
+
+    `rounding` is where the oracle's attention rounds its weights to bf16: "flash" rounds the
+    unnormalised p and divides by the fp32 sum, as the kernel does; "normalized" rounds the
+    normalised weights, the reference's point (src/deciax/kernels/attention/blocked.py:27)."""
     import torch
 
     from deciax_amd import gemma
@@ -116,7 +120,7 @@ def check_forward(name: str, weights, batch) -> ForwardParity:
     worst_l2 = worst_max = 0.0
     for i in range(cfg.layers):
         p = weights.numpy_layer(i)
-        args = (p, s, i, starts, batch.lengths, pos, cos, sin)
+        args = (p, s, i, starts, batch.lengths, pos, cos, sin, True, rounding)
         with accumulation(np.float64):
             forced = om.layer(xs[i], *args)
             truth = om.layer(truth, *args)

@@ -51,20 +51,23 @@ def test_tiny_forward_matches_oracle(lengths: list[int]) -> None:
     check_forward(f"tiny {lengths}", w, gemma.pack_batch(ids, options))
 
 
-def test_9b_shape_two_layers_matches_oracle() -> None:
-    """The 9B shape (H 3584, 16/8 x 256, MLP 14336, vocab 256000) through one sliding and one global layer."""
+@pytest.mark.parametrize("rounding", ["flash", "normalized"])
+def test_9b_shape_two_layers_matches_oracle(rounding: str) -> None:
+    """The 9B shape (H 3584, 16/8 x 256, MLP 14336, vocab 256000) through one sliding and one global layer,
+    against the oracle with either bf16 rounding point of the attention weights."""
     from dataclasses import replace
 
     from deciax_amd import gemma
 
-    say("9b-shaped decision forward, 2 layers")
+    say(f"9b-shaped decision forward, 2 layers, {rounding} attention rounding")
     cfg = replace(gemma.CONFIGS["gemma2-9b"], layers=2)
     w = gemma.random_weights(cfg, seed=2, keep_unpacked=True, norm_std=0.3)
     ids, options = _batch([333, 96], cfg.vocab, 8, seed=5)
-    check_forward("9b shape, 2 layers", w, gemma.pack_batch(ids, options))
+    check_forward(f"9b shape, 2 layers, {rounding} rounding", w, gemma.pack_batch(ids, options), rounding=rounding)
 
 
-def test_27b_shape_two_layers_matches_oracle() -> None:
+@pytest.mark.parametrize("rounding", ["flash", "normalized"])
+def test_27b_shape_two_layers_matches_oracle(rounding: str) -> None:
     """The 27B shape (H 4608, 32/16 heads x 128, query scale 1/sqrt(144), MLP 36864, vocab 256000)
     through one sliding and one global layer; one request crosses a small window so the sliding
     mask bites."""
@@ -72,11 +75,12 @@ def test_27b_shape_two_layers_matches_oracle() -> None:
 
     from deciax_amd import gemma
 
-    say("27b-shaped decision forward, 2 layers, window 128")
+    say(f"27b-shaped decision forward, 2 layers, window 128, {rounding} attention rounding")
     cfg = replace(gemma.CONFIGS["gemma2-27b"], layers=2, window=128)
     w = gemma.random_weights(cfg, seed=4, keep_unpacked=True, norm_std=0.3)
     ids, options = _batch([301, 77], cfg.vocab, 6, seed=9)
-    check_forward("27b shape, 2 layers, window 128", w, gemma.pack_batch(ids, options))
+    check_forward(f"27b shape, 2 layers, window 128, {rounding} rounding", w, gemma.pack_batch(ids, options),
+                  rounding=rounding)
 
 
 @pytest.mark.parametrize("model,lengths", [("gemma2-9b", [96, 40]), ("gemma2-27b", [64, 32])])
