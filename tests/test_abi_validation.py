@@ -123,3 +123,23 @@ def test_noalloc_attention_refuses_oversize_before_any_launch() -> None:
     assert b"static scratch" in lib().dx_last_error()
     check("dx_attn_prefill_noalloc", _lib.DX_OK, P, P, P, P, P, P, 0, 4096, 16, 8, 256, 4096, 2048, 2048, 4096,
           f(0.0625), f(50.0), 0, 1, _lib.DX_BF16, NUL)
+
+
+def test_linear_residual_norm_validation() -> None:
+    def lrn(m=8, d=512, k=256, lda=256, ldw=256, h=P, next_w=P, counters=P, post_w=P):
+        return ("dx_linear_residual_norm", P, P, P, P, post_w, next_w, h, counters, m, d, k, lda, ldw, 1e-6, NUL)
+
+    name = lrn()[0]
+    check(name, _lib.DX_ERR_INVALID, *lrn(post_w=NUL)[1:])
+    check(name, _lib.DX_ERR_INVALID, *lrn(counters=NUL)[1:])
+    check(name, _lib.DX_ERR_INVALID, *lrn(h=NUL)[1:])                    # h without next_w's partner
+    check(name, _lib.DX_ERR_UNSUPPORTED, *lrn(d=320)[1:])                # d % 256
+    check(name, _lib.DX_ERR_UNSUPPORTED, *lrn(d=6400)[1:])               # d above 6144
+    check(name, _lib.DX_ERR_UNSUPPORTED, *lrn(k=200, lda=200, ldw=200)[1:])
+    check(name, _lib.DX_ERR_INVALID, *lrn(lda=128)[1:])                  # lda below k
+    check(name, _lib.DX_ERR_INVALID, *lrn(counters=ctypes.c_void_p(0x10002))[1:])
+    check(name, _lib.DX_OK, *lrn(m=0)[1:])
+    check(name, _lib.DX_OK, *lrn(m=0, h=NUL, next_w=NUL)[1:])
+    assert lib().dx_linear_residual_norm_counters(0) == 0
+    assert lib().dx_linear_residual_norm_counters(70471) == (70471 + 255) // 256
+    assert lib().dx_linear_residual_norm_counters(1000) == (1000 + 127) // 128
