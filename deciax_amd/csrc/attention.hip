@@ -1,4 +1,5 @@
-// Causal GQA prefill attention for gfx950 (bf16 MFMA path and an fp32 path).
+// Causal GQA prefill attention for gfx950: a bf16 MFMA path, an fp32 MFMA path (head_dim <= 128) and
+// an fp32 VALU path (head_dim 256).
 //
 // Algorithm (the reference's blocked causal GQA attention,
 // src/deciax/kernels/attention/blocked.py:9-32, in the online form of its TPU
@@ -491,6 +492,218 @@ attn_f32_kernel(const float *__restrict__ Q, const float *__restrict__ K, const 
   }
 }
 
+// fp32 path on the matrix core, head_dim <= 128: v_mfma_f32_32x32x2_f32 (fp32 products and sums).
+// A workgroup takes 32 query rows of one head. Its F_WAVES waves split the 32-key blocks (wave w takes
+// blocks w, w + F_WAVES, ...), each staging its block in an LDS region of its own, and merge their
+// online-softmax states (running max, row sum, O) at the end, so no barrier runs inside the key loop.
+//   S^T = K Q^T: D / 2 MFMAs, MFMA j contracting head dims j (lanes 0-31) and D / 2 + j (lanes
+//   32-63). Lane l then holds query l % 32 and keys (r / 4) 8 + (l / 32) 4 + r % 4 of the block.
+//   O^T += V^T P^T: MFMA step i contracts the two keys the lane halves hold in register i, so each lane
+//   feeds its own probabilities as the B operand and reads V[key][d] for its half's key.
+// The next block's K and V come from global memory into registers during this block's QK^T and
+// softmax / PV respectively, and go to LDS once the region's previous reads are done (LDS operations of
+// one wave complete in order).
+constexpr int F_WAVES = 4;
+
+DX_DEVICE floatx16 mfma32_f32(float a, float b, floatx16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+}
+
+template <int D>
+__global__ void __launch_bounds__(64 * F_WAVES) __attribute__((amdgpu_waves_per_eu(1, 1)))
+attn_f32_mfma_kernel(const float *__restrict__ Q, const float *__restrict__ K, const float *__restrict__ V,
+                     float *__restrict__ O, const int32_t *__restrict__ seq_start, const int32_t *__restrict__ seq_len,
+                     int max_seq_len, int hq, int hkv, long q_stride, long k_stride, long v_stride, long o_stride,
+                     float scale, float softcap, int window, int causal, const uint8_t *__restrict__ key_mask) {
+  static_assert(D == 64 || D == 128, "fp32 matrix-core attention covers head_dim 64 and 128");
+  constexpr int KP = D + 4;    // K row pitch (floats): 16 lanes reading 16 bytes of 16 rows cover all 64 banks
+  constexpr int VP = D + 8;    // V row pitch: the lane halves read rows 4 apart, on disjoint banks
+  constexpr int REGION = 32 * KP + 32 * VP;  // floats per wave
+  constexpr int DH = D / 2;
+  constexpr int NDB = D / 32;
+  constexpr int LPL = 32 * (D / 4) / 64;     // 16-byte chunks of a 32 x D block per lane
+  constexpr int OP = 33;                     // merge: O^T [D][32] at pitch 33, then m [32] and l [32]
+  static_assert(D * OP + 64 <= REGION, "merge state fits the wave's region");
+  __shared__ __attribute__((aligned(16))) float smem[F_WAVES * REGION];
+
+  const int b = blockIdx.y, h = blockIdx.z, g = h / (hq / hkv);
+  const int len = min(max(seq_len[b], 0), max_seq_len);
+  const int ntiles = (max_seq_len + 31) / 32;
+  const int q0 = (ntiles - 1 - (int)blockIdx.x) * 32;  // heaviest (last) query tiles first
+  if (q0 >= len) return;
+  const long start = seq_start[b];
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lrow = lane & 31, hh = lane >> 5;
+  const int qi = q0 + lrow;
+  float *const ks = smem + wave * REGION;
+  float *const vs = ks + 32 * KP;
+
+  float qf[DH];
+  {
+    const float *qp = Q + (start + min(qi, len - 1)) * q_stride + (long)h * D + hh * DH;
+#pragma unroll
+    for (int j = 0; j < DH; j += 4) {
+      const float4 v = *reinterpret_cast<const float4 *>(qp + j);
+      qf[j] = v.x;
+      qf[j + 1] = v.y;
+      qf[j + 2] = v.z;
+      qf[j + 3] = v.w;
+    }
+  }
+  const int qlast = min(q0 + 31, len - 1);
+  int klo, khi;
+  if (causal) {
+    khi = qlast + 1;
+    klo = window > 0 ? max(0, q0 - window + 1) : 0;
+  } else {
+    khi = window > 0 ? min(len, qlast + window + 1) : len;
+    klo = window > 0 ? max(0, q0 - window) : 0;
+  }
+  const int kb0 = klo / 32, kb1 = (khi + 31) / 32;
+
+  // chunk c = lane + 64 t of a block: key row c / (D / 4) = t RPT + lane / (D / 4), columns
+  // 4 (lane % (D / 4)) .. + 3. Each block's K and V rows come through buffer resources based at the
+  // block's first key, so the per-lane offsets are loop-invariant and rows past the sequence read zeros
+  // (their scores are masked).
+  constexpr int RPT = 64 / (D / 4);  // key rows per chunk step t
+  const int crow = lane / (D / 4), ccol = (lane % (D / 4)) * 4;
+  const int koff = (int)((crow * k_stride + ccol) * 4), voff = (int)((crow * v_stride + ccol) * 4);
+  const float *const kseq = K + start * k_stride + (long)g * D;
+  const float *const vseq = V + start * v_stride + (long)g * D;
+  float4 kr[LPL], vr[LPL];
+  auto rsrc = [&](const float *base, long stride, int kb) {
+    const long rows = max(len - kb * 32, 0);
+    return __builtin_amdgcn_make_buffer_rsrc((void *)(base + (long)kb * 32 * stride), (short)0,
+                                             (int)(rows * stride * 4), 0x00020000);
+  };
+  auto fetch_k = [&](int kb) {
+    const __amdgpu_buffer_rsrc_t r = rsrc(kseq, k_stride, kb);
+#pragma unroll
+    for (int t = 0; t < LPL; ++t)
+      kr[t] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, koff, (int)(t * RPT * k_stride * 4), 0));
+  };
+  auto fetch_v = [&](int kb) {
+    const __amdgpu_buffer_rsrc_t r = rsrc(vseq, v_stride, kb);
+#pragma unroll
+    for (int t = 0; t < LPL; ++t)
+      vr[t] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, (int)(t * RPT * v_stride * 4), 0));
+  };
+  auto put_k = [&]() {
+#pragma unroll
+    for (int t = 0; t < LPL; ++t) *reinterpret_cast<float4 *>(ks + (t * RPT + crow) * KP + ccol) = kr[t];
+  };
+  auto put_v = [&]() {
+#pragma unroll
+    for (int t = 0; t < LPL; ++t) *reinterpret_cast<float4 *>(vs + (t * RPT + crow) * VP + ccol) = vr[t];
+  };
+
+  floatx16 o[NDB];
+#pragma unroll
+  for (int i = 0; i < NDB; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o[i][r] = 0.f;
+  float m = NEG_BIG, l = 0.f;  // running max (log2 units) and this lane's share of the row sum
+  const float cap2 = softcap > 0.f ? 2.f * LOG2E / softcap : 0.f;
+
+  int kb = kb0 + wave;
+  if (kb < kb1) {
+    fetch_k(kb);
+    put_k();
+    fetch_v(kb);
+  }
+  for (; kb < kb1; kb += F_WAVES) {
+    put_v();
+    const int nb = kb + F_WAVES;
+    const bool more = nb < kb1;
+    if (more) fetch_k(nb);
+    floatx16 s;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) s[r] = 0.f;
+    {
+      const float *kp = ks + lrow * KP + hh * DH;
+#pragma unroll
+      for (int j = 0; j < DH; j += 4) {
+        const float4 kv = *reinterpret_cast<const float4 *>(kp + j);
+        s = mfma32_f32(kv.x, qf[j], s);
+        s = mfma32_f32(kv.y, qf[j + 1], s);
+        s = mfma32_f32(kv.z, qf[j + 2], s);
+        s = mfma32_f32(kv.w, qf[j + 3], s);
+      }
+    }
+    if (more) {
+      put_k();
+      fetch_v(nb);
+    }
+    // score r is key kb 32 + (r / 4) 8 + 4 hh + r % 4 of query qi
+    const int kbase = kb * 32 + 4 * hh;
+    uint32_t vis = 0;
+    float tmax = NEG_BIG;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int key = kbase + (r >> 2) * 8 + (r & 3);
+      float x = s[r] * scale;
+      if (softcap > 0.f) x = softcap - 2.f * softcap * fast_rcp(1.f + fast_exp2(x * cap2));  // cap tanh(x / cap)
+      x *= LOG2E;
+      const bool v = visible(qi, key, len, window, causal) && (!key_mask || key_mask[start + key]);
+      vis |= (uint32_t)v << r;
+      s[r] = x;
+      if (v) tmax = fmaxf(tmax, x);
+    }
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+    const float mnew = fmaxf(m, tmax);
+    const float alpha = fast_exp2(m - mnew);
+    m = mnew;
+    l *= alpha;
+    if (__builtin_amdgcn_ballot_w64(alpha != 1.f)) {  // some row's running max moved
+#pragma unroll
+      for (int i = 0; i < NDB; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[i][r] *= alpha;
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const float p = ((vis >> r) & 1u) ? fast_exp2(s[r] - mnew) : 0.f;
+      s[r] = p;
+      l += p;
+    }
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+      for (int i = 0; i < 16; ++i)
+        o[db] = mfma32_f32(vs[((i >> 2) * 8 + 4 * hh + (i & 3)) * VP + db * 32 + lrow], s[i], o[db]);
+  }
+
+  // merge the waves' states: wave w writes O^T, m and the row sum into its region, then every thread
+  // combines (query, head-dim) elements, consecutive threads taking consecutive head dims
+  l += __shfl_xor(l, 32, 64);
+  __syncthreads();  // every wave is done with its K / V region
+#pragma unroll
+  for (int db = 0; db < NDB; ++db)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) ks[(db * 32 + (r >> 2) * 8 + 4 * hh + (r & 3)) * OP + lrow] = o[db][r];
+  if (hh == 0) {
+    ks[D * OP + lrow] = m;
+    ks[D * OP + 32 + lrow] = l;
+  }
+  __syncthreads();
+  for (int idx = tid; idx < 32 * D; idx += 64 * F_WAVES) {
+    const int q = idx / D, d = idx % D;
+    if (q0 + q >= len) continue;
+    float mx = NEG_BIG;
+#pragma unroll
+    for (int w = 0; w < F_WAVES; ++w) mx = fmaxf(mx, smem[w * REGION + D * OP + q]);
+    float acc = 0.f, sum = 0.f;
+#pragma unroll
+    for (int w = 0; w < F_WAVES; ++w) {
+      const float *st = smem + w * REGION;
+      const float f = fast_exp2(st[D * OP + q] - mx);
+      acc += st[d * OP + q] * f;
+      sum += st[D * OP + 32 + q] * f;
+    }
+    O[(start + q0 + q) * o_stride + (long)h * D + d] = sum > 0.f ? acc / sum : 0.f;  // no visible key: zeros
+  }
+}
+
 // V rows -> V^T tiles. Grid: (64-row tiles of the longest sequence, sequences,
 // kv heads x D/64). Rows past seq_len up to the next multiple of 64 are
 // written as zeros, so P.V never multiplies a zero probability by stale data.
@@ -585,6 +798,16 @@ hipError_t launch_f32_d(const AttnArgs &a, hipStream_t s) {
   return hipGetLastError();
 }
 
+template <int D>
+hipError_t launch_f32_mfma_d(const AttnArgs &a, hipStream_t s) {
+  const dim3 grid((a.max_seq_len + 31) / 32, a.num_seqs, a.hq);
+  attn_f32_mfma_kernel<D><<<grid, dim3(64 * F_WAVES), 0, s>>>(
+      static_cast<const float *>(a.q), static_cast<const float *>(a.k), static_cast<const float *>(a.v),
+      static_cast<float *>(a.out), a.seq_start, a.seq_len, a.max_seq_len, a.hq, a.hkv, a.q_stride, a.k_stride,
+      a.v_stride, a.out_stride, a.scale, a.softcap, a.window, a.causal, a.key_mask);
+  return hipGetLastError();
+}
+
 // Thread t packs word t % words of sequence t / words: bit j <- key_mask[seq_start + 32 w + j] != 0 for keys
 // inside the sequence, 0 past its length.
 __global__ void __launch_bounds__(THREADS)
@@ -625,10 +848,10 @@ hipError_t dx_attn_bf16(const AttnArgs &a, hipStream_t s) {
 
 hipError_t dx_attn_f32(const AttnArgs &a, hipStream_t s) {
   switch (a.d) {
-    // 8 to 16 threads per query: the reference's fp32 case (1 x 512, 8 heads) then fills 256 workgroups
-    // instead of 32 (378 -> 167 us at head_dim 128)
-    case 64: return launch_f32_d<64, 8>(a, s);
-    case 128: return launch_f32_d<128, 16>(a, s);
+    case 64: return launch_f32_mfma_d<64>(a, s);
+    case 128: return launch_f32_mfma_d<128>(a, s);
+    // head_dim 256 keeps the VALU kernel (the matrix-core one would hold 128 query registers per lane),
+    // 16 threads per query
     case 256: return launch_f32_d<256, 16>(a, s);
   }
   return hipErrorInvalidValue;
