@@ -572,7 +572,7 @@ attn_f32_mfma_kernel(const float *__restrict__ Q, const float *__restrict__ K, c
   const float *const vseq = V + start * v_stride + (long)g * D;
   float4 kr[LPL], vr[LPL];
   auto rsrc = [&](const float *base, long stride, int kb) {
-    const long rows = max(len - kb * 32, 0);
+    const long rows = min(max(len - kb * 32, 0), 32);  // the block's rows only: 32-bit byte counts
     return __builtin_amdgcn_make_buffer_rsrc((void *)(base + (long)kb * 32 * stride), (short)0,
                                              (int)(rows * stride * 4), 0x00020000);
   };

@@ -110,6 +110,11 @@ def test_attention_32bit_ranges_refused() -> None:
     assert packed(2048, 4096) == _lib.DX_ERR_UNSUPPORTED
     assert b"2 GiB" in lib().dx_last_error()
 
+    # fp32: a 32-key block of K or V is read through 32-bit byte offsets, so row strides stop at 2^24
+    fp32 = status("dx_attn_prefill", P, P, P, P, P, P, 1, 64, 8, 4, 128, 1024, 1 << 24, 512, 1024,
+                  f(0.088), f(0.0), 0, 1, _lib.DX_F32, NUL, 0, NUL)
+    assert fp32 == _lib.DX_ERR_UNSUPPORTED and b"2^24" in lib().dx_last_error()
+
 
 def test_noalloc_attention_refuses_oversize_before_any_launch() -> None:
     """dx_attn_prefill_noalloc stages V^T in a static scratch of DX_NOALLOC_SCRATCH_BYTES; a call that
