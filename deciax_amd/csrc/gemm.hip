@@ -62,7 +62,11 @@ struct Int {
 };
 
 constexpr int BK = 64;
-constexpr int BN = 256;
+// Column tile: 256, or 128 for the 64-row tiles that serve small M (plain epilogues only). Every output
+// element runs the same MFMA chain in the same k order in either shape, so its value does not depend on
+// the tile configuration, hence not on M.
+template <int BM>
+constexpr int tile_n() { return BM == 64 ? 128 : 256; }
 constexpr int THREADS = 256;
 
 enum { EPI_BF16 = 0, EPI_F32 = 1, EPI_GATED = 2, EPI_QKV = 3, EPI_NORM = 4 };
@@ -160,12 +164,16 @@ template <int BM, int EPI, bool DTL>
 __global__ void __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(1, 1)))
 gemm_nt_kernel(const uint16_t *__restrict__ A, const uint16_t *__restrict__ B, void *__restrict__ C, int M, int N,
                int K, long lda, long ldb, long ldc, int act, int group_m, QkvEpilogue qe, NormEpilogue ne) {
+  constexpr int BN = tile_n<BM>();
   constexpr int TM = BM / 64, TN = BN / 64;  // 32x32 blocks per wave along m, n
+  // the narrow tiles have too few MFMAs per k-step for the fixed-slot schedules: the compiler schedules them
+  constexpr bool SMALL = BM == 64;
+  static_assert(!SMALL || EPI == EPI_BF16 || EPI == EPI_F32, "narrow tiles take the plain epilogues only");
   constexpr int STAGE = (BM + BN) * BK;
   constexpr int AC = BM * BK / 8 / THREADS, BC = BN * BK / 8 / THREADS;  // 16-byte chunks per thread
   constexpr int NC = AC + BC;
   constexpr int RATIO = NC / AC;  // chunk j is an A chunk iff j % RATIO == 0
-  static_assert(NC % 4 == 0 && NC % AC == 0, "chunk schedule");
+  static_assert((SMALL || NC % 4 == 0) && NC % AC == 0, "chunk schedule");
   constexpr int OUT_W = EPI == EPI_GATED ? BN / 2 : BN;
   constexpr int OUT_PITCH = OUT_W + 8;
   // 256-row direct-to-LDS tiles use a ring of 3 A and 2 B stages (5 x 32 KB = the whole 160 KB)
@@ -272,9 +280,9 @@ gemm_nt_kernel(const uint16_t *__restrict__ A, const uint16_t *__restrict__ B, v
   constexpr int GS = NM / NG;                          // MFMAs between two loads
   constexpr int W0 = (NC + 2) / 3, W1 = (NC + 1) / 3;  // writes per pre-barrier k-step
   constexpr int R0 = BM == 256 ? 6 : NM / 4;          // first fragment-read slot
-  static_assert(GS >= 2 && W0 <= NM && R0 + NR <= NM, "region schedule");
+  static_assert(SMALL || (GS >= 2 && W0 <= NM && R0 + NR <= NM), "region schedule");
 #define DX_REGION(nw, ng)                                                                          \
-  do {                                                                                             \
+  if constexpr (!SMALL) do {                                                                       \
     _Pragma("unroll") for (int t = 0; t < NM; ++t) {                                               \
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                                           \
       if (t < (nw)) __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);                             \
@@ -385,9 +393,9 @@ gemm_nt_kernel(const uint16_t *__restrict__ A, const uint16_t *__restrict__ B, v
     // their stage and half (P0) in the next k-step, at evenly spaced MFMA slots.
     constexpr int P3 = NI / 2, P0 = NI - NI / 2, P1 = NI - P3 - P0;
     constexpr int DR0 = R0;
-    static_assert(P1 >= 0 && DR0 + NR <= NM, "load schedule");
+    static_assert(P1 >= 0 && (SMALL || DR0 + NR <= NM), "load schedule");
 #define DX_DREGION(nl)                                                                             \
-  do {                                                                                             \
+  if constexpr (!SMALL) do {                                                                       \
     _Pragma("unroll") for (int t = 0; t < NM; ++t) {                                               \
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                                           \
       if ((t * (nl)) % NM < (nl)) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);               \
@@ -684,7 +692,7 @@ gemm_nt_kernel(const uint16_t *__restrict__ A, const uint16_t *__restrict__ B, v
 template <int BM, int EPI>
 hipError_t launch(const uint16_t *A, const uint16_t *B, void *C, long M, long N, long K, long lda, long ldb,
                   long ldc, int act, const QkvEpilogue &qe, const NormEpilogue &ne, hipStream_t s) {
-  const long num_m = (M + BM - 1) / BM, num_n = N / BN;
+  const long num_m = (M + BM - 1) / BM, num_n = N / tile_n<BM>();
   // 256-row tiles always take the direct-to-LDS ring: its A stages give long-K shapes the latency slack
   // (against the register-staged path: down K 14336 +3-8 % alone and -0.8 % step time in the 9B
   // forward, K 36864 +4.5 %, 1344- and 448-tile down shapes +2.5 % / +1 %). 128-row tiles (M <= 1024)
@@ -706,7 +714,12 @@ template <int EPI>
 hipError_t dispatch(const uint16_t *A, const uint16_t *B, void *C, long M, long N, long K, long lda, long ldb,
                     long ldc, int act, hipStream_t s, const QkvEpilogue &qe = QkvEpilogue{},
                     const NormEpilogue &ne = NormEpilogue{}) {
-  // Small M: halve the row tile so more workgroups exist.
+  // Small M: halve the row tile so more workgroups exist. For the plain epilogues, 64 x 128 tiles when the
+  // 128 x 256 ones would leave three quarters of the CUs idle (under 64 tiles: o and down of one 9B
+  // request of up to 512 tokens; its forward -12 to -16% at 128-512 tokens, unchanged from 768 on).
+  if constexpr (EPI == EPI_BF16 || EPI == EPI_F32)
+    if (M <= 1024 && (M + 127) / 128 * (N / tile_n<128>()) < 64)
+      return launch<64, EPI>(A, B, C, M, N, K, lda, ldb, ldc, act, qe, ne, s);
   if (M <= 1024) return launch<128, EPI>(A, B, C, M, N, K, lda, ldb, ldc, act, qe, ne, s);
   return launch<256, EPI>(A, B, C, M, N, K, lda, ldb, ldc, act, qe, ne, s);
 }

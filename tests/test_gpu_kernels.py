@@ -59,6 +59,27 @@ def test_linear_bf16(m: int, n: int, k: int) -> None:
     assert (got == want).mean() > 0.95
 
 
+@pytest.mark.parametrize("n,k", [(3584, 4096), (3584, 14336), (1024, 2048)])
+def test_linear_rows_do_not_depend_on_m(n: int, k: int) -> None:
+    """Small M takes other tile shapes (64 x 128 below 64 standard tiles, 128 x 256 up to 1024 rows,
+    256 x 256 above), and long K another load path; every row must still equal the same row of a
+    4096-row product, bf16 and fp32 out, so a request's result does not depend on its batch."""
+    import torch
+
+    from deciax_amd import kernels as K
+
+    r = rng(n + k)
+    a = to_dev(bf16_np(r.normal(size=(4096, k)).astype(np.float32)))
+    w = to_dev(bf16_np(r.normal(size=(n, k)).astype(np.float32) * 0.02))
+    for dtype in (torch.bfloat16, torch.float32):
+        big = K.linear(a, w, out_dtype=dtype)
+        for m in (1, 37, 256, 300, 512, 640, 1024, 1500):
+            say(f"linear rows: M={m} N={n} K={k} {dtype}")
+            small = K.linear(a[:m].contiguous(), w, out_dtype=dtype)
+            torch.cuda.synchronize()
+            assert torch.equal(small, big[:m]), f"M={m} N={n} K={k} {dtype}: rows differ from the 4096-row product"
+
+
 def test_linear_f32_and_strides() -> None:
     import torch
 
