@@ -224,3 +224,32 @@ def test_full_size_batch_order_invariance(model: str) -> None:
         for q in options[i]:
             assert abs(float(forward[i][1][offset:offset + len(q)].sum()) - 1.0) < 1e-5
             offset += len(q)
+
+
+@pytest.mark.parametrize("model", ["gemma2-9b", "gemma2-27b"])
+def test_request_alone_equals_request_in_batch(model: str) -> None:
+    """A request's logits and probabilities are bit-identical alone and inside a larger batch, across
+    the switches between tile shapes that follow the row count (64 x 128 plain-epilogue tiles for one
+    short request, 128-row tiles up to 1024 rows, 256-row tiles above) and between the attention grid
+    orders (batches up to 4096 tokens per sequence launch tile-major): every GEMM row, norm row,
+    attention row and readout question depends only on its own request. Full depth."""
+    from deciax_amd import gemma
+
+    cfg = gemma.CONFIGS[model]
+    w = gemma.random_weights(cfg, seed=3)
+    lengths = [300, 2100, 1500, 77]  # request 0 alone: 300 rows; in the batch: 3977 rows
+    ids, options = _batch(lengths, cfg.vocab, questions=4, seed=17)
+
+    def run(idx: list[int]):
+        batch = gemma.pack_batch([ids[i] for i in idx], [options[i] for i in idx])
+        logits, probs = gemma.forward(w, batch, gemma.Workspace(cfg, batch.rows, batch.vt_ld, w.device))
+        return logits.cpu().numpy(), probs.cpu().numpy()
+
+    n0 = sum(len(q) for q in options[0])
+    say(f"request alone vs in a batch, {model}: {lengths[0]} rows vs {sum(lengths)}")
+    alone = run([0])
+    for order in ([1, 0, 2, 3], [0, 1, 2, 3], [3, 2, 1, 0]):
+        together = run(order)
+        offset = sum(sum(len(q) for q in options[i]) for i in order[:order.index(0)])
+        for a, b, what in ((alone[0], together[0], "logits"), (alone[1], together[1], "probabilities")):
+            assert np.array_equal(a, b[offset:offset + n0]), f"{model}: {what} of request 0 depend on its batch {order}"
