@@ -25,9 +25,6 @@ DX_DEVICE uint16_t f2bf(float f) {
   return __builtin_bit_cast(uint16_t, b);
 }
 
-// Round an fp32 value to the nearest bf16 and return it as fp32.
-DX_DEVICE float round_bf(float f) { return bf2f(f2bf(f)); }
-
 // Two fp32 values -> one dword of two bf16 (lo in the low half).
 DX_DEVICE uint32_t pack_bf2(float lo, float hi) {
   typedef float floatx2 __attribute__((ext_vector_type(2)));
@@ -35,6 +32,10 @@ DX_DEVICE uint32_t pack_bf2(float lo, float hi) {
   const floatx2 v = {lo, hi};
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));  // one v_cvt_pk_bf16_f32
 }
+
+// Round an fp32 value to the nearest bf16 and return it as fp32: the bf16 in the high half over a zero low
+// half is that value's fp32 bit pattern, so this is one conversion and no shift.
+DX_DEVICE float round_bf(float f) { return __uint_as_float(pack_bf2(0.f, f)); }
 
 DX_DEVICE float lo_bf(uint32_t w) { return __uint_as_float(w << 16); }
 DX_DEVICE float hi_bf(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }

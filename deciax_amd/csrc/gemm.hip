@@ -563,8 +563,8 @@ gemm_nt_kernel(const uint16_t *__restrict__ A, const uint16_t *__restrict__ B, v
           for (int j = 0; j < TN / 2; ++j)
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
-              // the bf16 roundings of g, u and act(g) go two values per conversion: pack_bf2 rounds like
-              // round_bf, and lo_bf / hi_bf return the two halves exactly
+              // g and u are rounded to bf16 two values per conversion (pack_bf2 rounds like round_bf, and
+              // lo_bf / hi_bf return the two halves exactly), act(g) one value per conversion (round_bf)
               const floatx16 &ga = acc[i][j], &ua = acc[i][j + TN / 2];
               const uint32_t g2[2] = {pack_bf2(ga[4 * q], ga[4 * q + 1]), pack_bf2(ga[4 * q + 2], ga[4 * q + 3])};
               const uint32_t u2[2] = {pack_bf2(ua[4 * q], ua[4 * q + 1]), pack_bf2(ua[4 * q + 2], ua[4 * q + 3])};
@@ -572,10 +572,10 @@ gemm_nt_kernel(const uint16_t *__restrict__ A, const uint16_t *__restrict__ B, v
 #pragma unroll
               for (int h = 0; h < 2; ++h) {
                 const float g0 = lo_bf(g2[h]), g1 = hi_bf(g2[h]);
-                const uint32_t a2 = decltype(silu_c)::value ? pack_bf2(silu(g0), silu(g1))
-                                                            : pack_bf2(gelu_tanh(g0), gelu_tanh(g1));
-                o[2 * h] = lo_bf(a2) * lo_bf(u2[h]);
-                o[2 * h + 1] = hi_bf(a2) * hi_bf(u2[h]);
+                const float a0 = round_bf(decltype(silu_c)::value ? silu(g0) : gelu_tanh(g0));
+                const float a1 = round_bf(decltype(silu_c)::value ? silu(g1) : gelu_tanh(g1));
+                o[2 * h] = a0 * lo_bf(u2[h]);
+                o[2 * h + 1] = a1 * hi_bf(u2[h]);
               }
               const int col = wn * (BN / 4) + j * 32 + q * 8 + lhalf * 4;
               u32x2 w;
