@@ -364,11 +364,13 @@ def config_kernels(reps: int = 5) -> dict:
 
 def decide_batch_throughput(weights, lengths: list[int], questions_per_request: int = QUESTIONS,
                             reps: int = 3) -> dict:
-    """End-to-end `decide_batch` on text requests whose encoded lengths equal the forward's batch: the
-    byte tokenizer's encoding of the prompt and schema, packing, the host-to-device copy of ids and
-    descriptors, the forward, the device-to-host copy and the decode, timed on the host clock
-    (median of `reps` after one warm-up call). Every request asks the same `questions_per_request`
-    choice questions of 2-8 options."""
+    """End-to-end `decide_batch` on text requests sized like the forward's batch: the byte tokenizer's
+    encoding of the prompt and schema, packing, the host-to-device copy of ids and descriptors, the
+    forward, the device-to-host copy and the decode, timed on the host clock (median of `reps` after
+    one warm-up call). Every request asks the same `questions_per_request` choice questions of 2-8
+    options. A request's encoded length is max(L, prompt and schema + 1) for the batch length L: the
+    fixed part (3256 tokens at 8 questions) exceeds the shortest lengths, so the call carries more
+    tokens than the forward's batch (`tokens` in the result)."""
     from deciax_amd.engine import DecisionEngine
     from deciax_amd.schema import ByteTokenizer, encode
 
