@@ -556,6 +556,38 @@ def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, key_mask: torch
     return out.contiguous()
 
 
+FLASH_HEAD_DIM = 64  # the reference TPU kernel's fixed head size (pallas.py:18)
+
+
+def flash_attention(qkv: torch.Tensor, mask: torch.Tensor, *, heads: int, window: int = 0,
+                    out_dtype: torch.dtype = BF16) -> torch.Tensor:
+    """Packed [B, S, 3 H 64] q | k | v and a [B, S] key mask (1 = real token) -> [B, S, H 64]: the
+    interface of the reference's TPU flash kernel (`flash_attention`,
+    src/deciax/kernels/attention/pallas.py:52-135). Bidirectional, one key head per query head,
+    head_dim 64, queries scaled by 64^-0.5 (exact: a power of two), keys with |q - k| <= window when
+    window > 0 (mask_bias, :31-39); online softmax in fp32 with P rounded to the value dtype for P.V
+    (pv_t, :47-49).
+
+    Differences from the reference, stated rather than copied: S need not be a multiple of its
+    256 / 512 blocks (it asserts that), shape errors raise ValueError (it asserts), and the output
+    takes the input's dtype (`out_dtype` must equal it)."""
+    if not isinstance(qkv, torch.Tensor) or qkv.dim() != 3:
+        raise ValueError("flash_attention: qkv must be [B, S, 3 * heads * 64]")
+    b, s, width = qkv.shape
+    if heads < 1 or width != 3 * heads * FLASH_HEAD_DIM:
+        raise ValueError(f"flash_attention: qkv width {width} is not 3 * {heads} heads * {FLASH_HEAD_DIM}")
+    if tuple(mask.shape) != (b, s):
+        raise ValueError(f"flash_attention: mask must be [{b}, {s}], got {tuple(mask.shape)}")
+    if window < 0:
+        raise ValueError("flash_attention: window must be >= 0")
+    if out_dtype != qkv.dtype:
+        raise ValueError(f"flash_attention: out_dtype must be the input dtype {qkv.dtype}, got {out_dtype}")
+    d = heads * FLASH_HEAD_DIM
+    q, k, v = (qkv[..., i * d:(i + 1) * d].reshape(b, s, heads, FLASH_HEAD_DIM) for i in range(3))
+    out = attention(q, k, v, mask, causal=False, window=window, scale=FLASH_HEAD_DIM ** -0.5)
+    return out.reshape(b, s, d)
+
+
 # ---------------------------------------------------------------------------- readout
 
 

@@ -424,6 +424,41 @@ def test_attention_arbitrary_key_mask(nq, nk, hq, hkv, d, causal, window, softca
             np.testing.assert_allclose(a[bi], want, rtol=1e-4, atol=1e-4)
 
 
+@pytest.mark.parametrize("b,s,heads,window,dtype", [(2, 200, 4, 0, "bf16"), (2, 257, 3, 32, "bf16"),
+                                                     (1, 96, 2, 8, "f32")])
+def test_flash_attention_packed_interface(b: int, s: int, heads: int, window: int, dtype: str) -> None:
+    """The reference TPU kernel's interface (src/deciax/kernels/attention/pallas.py:52-135): packed
+    [B, S, 3 H 64] q | k | v, a [B, S] key mask with padded tails, bidirectional, |q - k| <= window.
+    Real-token rows against the oracle (the reference's test compares only those,
+    tests/kernels/test_attention.py:42): 2e-2 in bf16 in both rounding forms, 1e-4 in fp32."""
+    import torch
+
+    from deciax_amd import kernels as K
+    from oracle.attention import attention_seq
+
+    say(f"flash_attention packed b={b} s={s} heads={heads} window={window} {dtype}")
+    r = rng(s + heads + window)
+    d = heads * 64
+    qkv = r.normal(size=(b, s, 3 * d)).astype(np.float32)
+    if dtype == "bf16":
+        qkv = bf16_np(qkv)
+    mask = np.ones((b, s), bool)
+    mask[-1, s - s // 3:] = False  # the last request is padded
+    got = to_np(K.flash_attention(to_dev(qkv, dtype), i32(mask.astype(np.int32)), heads=heads, window=window,
+                                  out_dtype=torch.bfloat16 if dtype == "bf16" else torch.float32))
+    assert got.shape == (b, s, d)
+    for bi in range(b):
+        q, k, v = (qkv[bi, :, i * d:(i + 1) * d].reshape(s, heads, 64) for i in range(3))
+        real = np.flatnonzero(mask[bi])
+        for rounding in (("flash", "normalized") if dtype == "bf16" else ("flash",)):
+            want = attention_seq(q, k, v, scale=0.125, window=window, causal=False, bf16=dtype == "bf16",
+                                 key_mask=mask[bi], query_pos=real, rounding=rounding).reshape(len(real), d)
+            if dtype == "bf16":
+                close(got[bi, real], want, 2e-2, MEAN_REL[rounding])
+            else:
+                np.testing.assert_allclose(got[bi, real], want, rtol=1e-4, atol=1e-4)
+
+
 @pytest.mark.parametrize("window", [4096, 0, 512])
 def test_attention_layer_pair_full_shape(window: int) -> None:
     """Gemma-2-9B attention layer at batch 8 x 2048, 16/8 heads x 256, softcap 50, scale 1/16: the

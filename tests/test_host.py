@@ -395,3 +395,24 @@ def test_bench_norm_bytes() -> None:
     t = 70471
     per = bench.algorithmic_bytes(cfg, [t])["add_rmsnorm"]
     assert per * 84 == 83 * 4 * 2 * t * 3584 + 3 * 2 * t * 3584
+
+
+def test_flash_attention_rejects_bad_shapes() -> None:
+    """The packed flash interface checks its shapes before any device work (ValueError where the
+    reference TPU kernel asserts, src/deciax/kernels/attention/pallas.py:70,73)."""
+    import torch
+
+    from deciax_amd import kernels as K
+
+    qkv = torch.zeros((2, 16, 3 * 2 * 64), dtype=torch.bfloat16)
+    mask = torch.ones((2, 16), dtype=torch.int32)
+    with pytest.raises(ValueError, match="width"):
+        K.flash_attention(qkv, mask, heads=3)
+    with pytest.raises(ValueError, match="mask"):
+        K.flash_attention(qkv, mask[:, :8], heads=2)
+    with pytest.raises(ValueError, match="window"):
+        K.flash_attention(qkv, mask, heads=2, window=-1)
+    with pytest.raises(ValueError, match="out_dtype"):
+        K.flash_attention(qkv, mask, heads=2, out_dtype=torch.float32)
+    with pytest.raises(ValueError, match="qkv"):
+        K.flash_attention(qkv[0], mask, heads=2)
