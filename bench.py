@@ -256,6 +256,8 @@ def config_kernels(reps: int = 5) -> dict:
       softcap 50, sliding window 4096 plus global; and the 27B pair at the same lengths (32/16 heads
       x 128, scale 1/sqrt(144));
     - fused MLP, bf16: 8192 rows, H 3584, I 14336, RMSNorm(1 + w) -> GELU-tanh gate|up -> down;
+    - the 9B gate|up and down GEMMs at the benchmark batch's 70471 rows, each beside hipBLASLt
+      (torch.matmul) on the same product as a yardstick;
     - the 27B readout: 2048 options (4 requests x 64 questions x 8) over 4 x 16384 rows of H 4608
       and the 256000-row embedding table.
     bf16 attention times the kernel on V already transposed (the forward's form, dx_attn_prefill_vt).
@@ -342,7 +344,19 @@ def config_kernels(reps: int = 5) -> dict:
     out["yardstick_hipblaslt_gemm_bf16_70471x28672x3584"] = {
         "ms": round(ms, 3), "tflops": round(fl / ms / 1e9, 2), "frac_bf16_peak": round(fl / ms * 1e3 / PEAK_BF16, 4),
         "note": "torch.matmul (hipBLASLt) plain GEMM of the same shape, a yardstick only"}
-    del x, gate_up, down, plain
+    del x, gate_up, plain
+    # the 9B down projection (K 14336) and hipBLASLt on the same product: both write the same bf16 output
+    act = torch.randn((t, f), generator=g, device="cuda").to(torch.bfloat16)
+    y = torch.empty((t, h), dtype=torch.bfloat16, device="cuda")
+    fl = 2.0 * t * h * f
+    ms = timed(lambda: K.linear(act, down, out=y))
+    out["gemm_down_bf16_70471x3584x14336"] = {"ms": round(ms, 3), "tflops": round(fl / ms / 1e9, 2),
+                                              "frac_bf16_peak": round(fl / ms * 1e3 / PEAK_BF16, 4)}
+    ms = timed(lambda: torch.matmul(act, down.t(), out=y))
+    out["yardstick_hipblaslt_gemm_bf16_70471x3584x14336"] = {
+        "ms": round(ms, 3), "tflops": round(fl / ms / 1e9, 2), "frac_bf16_peak": round(fl / ms * 1e3 / PEAK_BF16, 4),
+        "note": "torch.matmul (hipBLASLt) of the same product, a yardstick only"}
+    del act, y, down
     # 27B readout: 4 requests x 16384 rows, 64 questions x 8 options in each request's last 512 rows
     h, rows, vocab, nreq, nq, per = 4608, 4 * 16384, 256000, 4, 64, 8
     hidden = torch.randn((rows, h), generator=g, device="cuda").to(torch.bfloat16)
