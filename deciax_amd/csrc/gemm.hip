@@ -160,7 +160,9 @@ DX_DEVICE void norm_epilogue(const uint16_t *Y, int M, int N, long ldy, int m0, 
   if (tid == 0) __hip_atomic_store(ne.counters + tm, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
-template <int BM, int EPI, bool DTL>
+// EB (256-row ring only): B's loads of the next tile all go before A's loads of the tile after it, so the
+// per-iteration wait leaves A's 8 loads in flight (see the ring schedule below).
+template <int BM, int EPI, bool DTL, bool EB = false>
 __global__ void __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(1, 1)))
 gemm_nt_kernel(const uint16_t *__restrict__ A, const uint16_t *__restrict__ B, void *__restrict__ C, int M, int N,
                int K, long lda, long ldb, long ldc, int act, int group_m, QkvEpilogue qe, NormEpilogue ne) {
@@ -299,6 +301,9 @@ gemm_nt_kernel(const uint16_t *__restrict__ A, const uint16_t *__restrict__ B, v
     // follow that barrier and 2 / 2 go in k-steps 0 / 1 of iteration T - 1. Every k-step thus
     // carries 4 loads per wave, one per 4 MFMAs (measured against the two-stage ring: +2-5% on the
     // 9B and 27B q|k|v, o and gate|up shapes, bit-identical results).
+    // With EB, B's second 4 loads all go in k-step 0 and A's 8 in k-steps 1 / 2 (4 / 4). The counter
+    // drains in issue order, so the wait that makes B of tile T + 1 visible then leaves all 8 A loads
+    // in flight, instead of waiting for A's first 4 as well: B gets about a k-step more to land.
     static_assert(AI == 8 && BI == 8, "ring schedule: 8 A and 8 B instructions per wave");
     constexpr int RS = BM * BK;  // elements per stage (A or B)
     auto la = [&](int kt, int sa, int j0, int j1) __attribute__((always_inline)) {
@@ -345,14 +350,22 @@ gemm_nt_kernel(const uint16_t *__restrict__ A, const uint16_t *__restrict__ B, v
       constexpr int q = decltype(qc)::value;
       constexpr int sa = q % 3, sb = q % 2, sa1 = (q + 1) % 3, sb1 = (q + 1) % 2, sa2 = (q + 2) % 3;
       __builtin_amdgcn_sched_barrier(0);
-      lb(cl(kt + 1), sb1, 4, 6);
-      la(cl(kt + 2), sa2, 0, 2);
+      if constexpr (EB) {
+        lb(cl(kt + 1), sb1, 4, 8);
+      } else {
+        lb(cl(kt + 1), sb1, 4, 6);
+        la(cl(kt + 2), sa2, 0, 2);
+      }
       rdr(fa1, fb1, sa, sb, 1);
       mm(fa0, fb0);
       DX_RREGION();
       __builtin_amdgcn_sched_barrier(0);
-      lb(cl(kt + 1), sb1, 6, 8);
-      la(cl(kt + 2), sa2, 2, 4);
+      if constexpr (EB) {
+        la(cl(kt + 2), sa2, 0, 4);
+      } else {
+        lb(cl(kt + 1), sb1, 6, 8);
+        la(cl(kt + 2), sa2, 2, 4);
+      }
       rdr(fa0, fb0, sa, sb, 2);
       mm(fa1, fb1);
       DX_RREGION();
@@ -362,9 +375,10 @@ gemm_nt_kernel(const uint16_t *__restrict__ A, const uint16_t *__restrict__ B, v
       mm(fa0, fb0);
       DX_RREGION();
       __builtin_amdgcn_sched_barrier(0);
-      // A and B of tile kt + 1 have landed (only this k-step's 4 loads may be younger), and every wave is
-      // done with tile kt, whose stages the next loads refill
-      asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)" ::: "memory");
+      // A and B of tile kt + 1 have landed (younger loads: this k-step's 4, or with EB the 8 of A's tile
+      // kt + 2), and every wave is done with tile kt, whose stages the next loads refill
+      if constexpr (EB) asm volatile("s_waitcnt vmcnt(8) lgkmcnt(0)" ::: "memory");
+      else asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)" ::: "memory");
       __builtin_amdgcn_s_barrier();
       __builtin_amdgcn_sched_barrier(0);
       lb(cl(kt + 2), sb, 0, 4);
@@ -700,6 +714,11 @@ hipError_t launch(const uint16_t *A, const uint16_t *B, void *C, long M, long N,
   auto kern = gemm_nt_kernel<BM, EPI, true>;
   if constexpr (BM != 256)
     if (K > 8192) kern = gemm_nt_kernel<BM, EPI, false>;
+  // The early-B order of the ring gains where the weight fits the 256 MB Infinity Cache (9B forward: gate|up
+  // +2.8%, down +1.9%, q|k|v +1.2%, step -1.7%) and loses where it does not (27B gate|up and down, 680 and
+  // 340 MB: -3% each); bit-identical either way.
+  if constexpr (BM == 256)
+    if (N * K * 2 <= (256L << 20)) kern = gemm_nt_kernel<BM, EPI, true, true>;
   // Tile rows walked together per XCD: 2 for long K, where an A row tile is megabytes and groups of 8
   // re-read it once per 4 column tiles (9B down, K 14336: +4%; K 36864: 0%); 4 for the plain bf16 /
   // fp32 epilogues (o at 9B and 27B: +1.5-2%); 8 for the gated and q|k|v epilogues, where 4 measured
