@@ -707,6 +707,7 @@ template <int BM, int EPI>
 hipError_t launch(const uint16_t *A, const uint16_t *B, void *C, long M, long N, long K, long lda, long ldb,
                   long ldc, int act, const QkvEpilogue &qe, const NormEpilogue &ne, hipStream_t s) {
   const long num_m = (M + BM - 1) / BM, num_n = N / tile_n<BM>();
+  const bool weight_cached = N * K * 2 <= (256L << 20);  // the weight fits the 256 MB Infinity Cache
   // 256-row tiles always take the direct-to-LDS ring: its A stages give long-K shapes the latency slack
   // (against the register-staged path: down K 14336 +3-8 % alone and -0.8 % step time in the 9B
   // forward, K 36864 +4.5 %, 1344- and 448-tile down shapes +2.5 % / +1 %). 128-row tiles (M <= 1024)
@@ -718,12 +719,15 @@ hipError_t launch(const uint16_t *A, const uint16_t *B, void *C, long M, long N,
   // +2.8%, down +1.9%, q|k|v +1.2%, step -1.7%) and loses where it does not (27B gate|up and down, 680 and
   // 340 MB: -3% each); bit-identical either way.
   if constexpr (BM == 256)
-    if (N * K * 2 <= (256L << 20)) kern = gemm_nt_kernel<BM, EPI, true, true>;
-  // Tile rows walked together per XCD: 2 for long K, where an A row tile is megabytes and groups of 8
-  // re-read it once per 4 column tiles (9B down, K 14336: +4%; K 36864: 0%); 4 for the plain bf16 /
-  // fp32 epilogues (o at 9B and 27B: +1.5-2%); 8 for the gated and q|k|v epilogues, where 4 measured
-  // mixed (27B q|k|v -4.7%).
-  const int group_m = K >= 8192 ? 2 : (EPI == EPI_BF16 || EPI == EPI_F32 || EPI == EPI_NORM) ? 4 : 8;
+    if (weight_cached) kern = gemm_nt_kernel<BM, EPI, true, true>;
+  // Tile rows walked together per XCD. Long K: an A row tile is megabytes, and groups of 8 re-read it
+  // once per 4 column tiles. So 1 row when the weight fits the Infinity Cache, where the weight's
+  // re-reads are cheap and the A tile's are not (9B down, K 14336: +1.3% against 2, +5% against 8), and
+  // 2 when it does not (27B down, K 36864: 1 and 3 within 0.2% of 2). 4 for the plain bf16 / fp32
+  // epilogues (o at 9B and 27B: +1.5-2%); 8 for the gated and q|k|v epilogues, where 4 measured mixed
+  // (27B q|k|v -4.7%).
+  const int group_m = K >= 8192 ? (weight_cached ? 1 : 2)
+                                : (EPI == EPI_BF16 || EPI == EPI_F32 || EPI == EPI_NORM) ? 4 : 8;
   kern<<<dim3((unsigned)(num_m * num_n)), dim3(THREADS), 0, s>>>(A, B, C, (int)M, (int)N, (int)K, lda, ldb, ldc,
                                                                  act, group_m, qe, ne);
   return hipGetLastError();
