@@ -724,10 +724,13 @@ hipError_t launch(const uint16_t *A, const uint16_t *B, void *C, long M, long N,
   // once per 4 column tiles. So 1 row when the weight fits the Infinity Cache, where the weight's
   // re-reads are cheap and the A tile's are not (9B down, K 14336: +1.3% against 2, +5% against 8), and
   // 2 when it does not (27B down, K 36864: 1 and 3 within 0.2% of 2). 4 for the plain bf16 / fp32
-  // epilogues (o at 9B and 27B: +1.5-2%); 8 for the gated and q|k|v epilogues, where 4 measured mixed
-  // (27B q|k|v -4.7%).
-  const int group_m = K >= 8192 ? (weight_cached ? 1 : 2)
-                                : (EPI == EPI_BF16 || EPI == EPI_F32 || EPI == EPI_NORM) ? 4 : 8;
+  // epilogues (o at 9B and 27B: +1.5-2%). 8 for the q|k|v epilogue, where 4 measured mixed (27B q|k|v
+  // -4.7%) and 6 too (9B +0.7%, 27B -1.2%). The gated epilogue takes 6 when its weight is cached (9B
+  // gate|up +1.1%) and 8 when not (27B gate|up: 6 is 10% slower).
+  const int short_k = (EPI == EPI_BF16 || EPI == EPI_F32 || EPI == EPI_NORM) ? 4
+                      : EPI == EPI_GATED && weight_cached                    ? 6
+                                                                             : 8;
+  const int group_m = K >= 8192 ? (weight_cached ? 1 : 2) : short_k;
   kern<<<dim3((unsigned)(num_m * num_n)), dim3(THREADS), 0, s>>>(A, B, C, (int)M, (int)N, (int)K, lda, ldb, ldc,
                                                                  act, group_m, qe, ne);
   return hipGetLastError();
