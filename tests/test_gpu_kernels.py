@@ -246,20 +246,31 @@ def test_attention_vt_path_matches_generic() -> None:
         assert (vt_np[:, p0 + n:p0 + (n + 63) // 64 * 64] == 0).all()
 
 
-@pytest.mark.parametrize("hq,hkv,d", [(16, 8, 256), (32, 16, 128)])
-@pytest.mark.parametrize("window", [4096, 0])
-def test_attention_long_sequences_and_descriptor_order(hq: int, hkv: int, d: int, window: int) -> None:
-    """Batches with a sequence longer than 4096 tokens take the (query tile, KV head, sequence) grid:
-    sampled rows of a 5000-token sequence (window 4096 active), a 4097- and a 300-token one against
-    the oracle; and the output is bit-identical when the sequence descriptors are listed longest
-    first, the order the forward driver uses."""
+LONG_CASES = [
+    # (hq, hkv, d, window, lengths): 24 or 48 (sequence, KV head) units, dealt out whole to the XCDs
+    (16, 8, 256, 4096, [300, 5000, 4097]),
+    (16, 8, 256, 0, [300, 5000, 4097]),
+    (32, 16, 128, 4096, [300, 5000, 4097]),
+    (32, 16, 128, 0, [300, 5000, 4097]),
+    (16, 8, 256, 0, [3100, 3500, 700]),   # just above the 3072-token switch
+    (8, 4, 128, 0, [300, 3500, 3100]),    # 12 units: not a multiple of 8, the plain order
+]
+
+
+@pytest.mark.parametrize("hq,hkv,d,window,lengths", LONG_CASES)
+def test_attention_long_sequences_and_descriptor_order(hq: int, hkv: int, d: int, window: int,
+                                                       lengths: list[int]) -> None:
+    """Batches with a sequence longer than 3072 tokens take the (query tile, KV head, sequence) grid,
+    with whole (sequence, KV head) units per XCD when their count is a multiple of 8: sampled rows of
+    every sequence (a 5000-token one with window 4096 active) against the oracle; and the output is
+    bit-identical when the sequence descriptors are listed longest first, the order the forward
+    driver uses."""
     import torch
 
     from deciax_amd import kernels as K
     from oracle.attention import attention_seq
 
-    say(f"attention long sequences hq={hq} hkv={hkv} d={d} window={window}")
-    lengths = [300, 5000, 4097]
+    say(f"attention long sequences hq={hq} hkv={hkv} d={d} window={window} lengths={lengths}")
     q, k, v, starts = _packed_case(5 + d + window, lengths, hq, hkv, d)
     rows = q.shape[0]
     qd, kd, vd = (to_dev(a.reshape(rows, -1)) for a in (q, k, v))
