@@ -366,10 +366,8 @@ def config_kernels(reps: int = 5) -> dict:
     pos = np.concatenate([b * 16384 + r.permutation(np.arange(16384 - nq * per, 16384)) for b in range(nreq)])
     opt_pos = torch.as_tensor(pos.astype(np.int32), device="cuda")
     opt_label = torch.as_tensor(r.integers(0, vocab, len(pos)).astype(np.int32), device="cuda")
-    q_off = torch.arange(0, len(pos) + 1, per, dtype=torch.int32, device="cuda")
-    q_off_host = q_off.cpu().tolist()
-    ms = timed(lambda: K.readout(hidden, fnorm, table, opt_pos, opt_label, q_off, eps=1e-6, softcap=30.0,
-                                 q_offsets_host=q_off_host))
+    q_off = K.offsets_tensor(range(0, len(pos) + 1, per), "cuda")
+    ms = timed(lambda: K.readout(hidden, fnorm, table, opt_pos, opt_label, q_off, eps=1e-6, softcap=30.0))
     nb = readout_bytes(h, len(pos), nreq * nq)
     out["readout_27b_2048_options"] = {"ms": round(ms, 4), "gbps": round(nb / ms / 1e6, 1),
                                        "frac_hbm_peak": round(nb / ms * 1e3 / PEAK_HBM, 4)}

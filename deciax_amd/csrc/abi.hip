@@ -531,6 +531,8 @@ int dx_readout(const void *hidden, const void *norm_w, const void *table, const 
           "readout: null pointer argument");
   REQUIRE(num_questions >= 0 && num_options >= 0 && hidden_rows > 0 && d > 0 && vocab > 0 && ld_hidden >= d,
           "readout: bad sizes");
+  REQUIRE(num_options <= INT32_MAX, "readout: num_options=%lld exceeds the int32 range of the offsets",
+          (long long)num_options);
   SUPPORTED(d % 8 == 0 && d <= 8192, "readout: d=%ld must be a multiple of 8 and <= 8192", (long)d);
   REQUIRE(ld_hidden % 8 == 0, "readout: ld_hidden must be a multiple of 8");
   REQUIRE(softcap >= 0.f, "readout: softcap must be >= 0");
@@ -538,9 +540,8 @@ int dx_readout(const void *hidden, const void *norm_w, const void *table, const 
   if (num_questions == 0) return DX_OK;
   return check_launch(dx_readout_launch(static_cast<const uint16_t *>(hidden), static_cast<const uint16_t *>(norm_w),
                                         static_cast<const uint16_t *>(table), opt_pos, opt_label, q_offsets,
-                                        num_questions, hidden_rows, (int)d, ld_hidden, vocab, eps, softcap, logits,
-                                        probs,
-                                        as_stream(stream)),
+                                        num_questions, (int)num_options, hidden_rows, (int)d, ld_hidden, vocab, eps,
+                                        softcap, logits, probs, as_stream(stream)),
                       "readout launch");
 }
 

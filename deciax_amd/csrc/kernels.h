@@ -81,9 +81,8 @@ hipError_t dx_rope_launch(uint16_t *x, const int32_t *pos, const uint16_t *cos, 
                           int heads, int d, long stride, int max_pos, hipStream_t s);
 hipError_t dx_readout_launch(const uint16_t *hidden, const uint16_t *norm_w, const uint16_t *table,
                              const int32_t *opt_pos, const int32_t *opt_label, const int32_t *q_off, int nq,
-                             long hidden_rows, int d,
-                             long ld_hidden, long vocab, float eps, float softcap, float *logits, float *probs,
-                             hipStream_t s);
+                             int num_options, long hidden_rows, int d, long ld_hidden, long vocab, float eps,
+                             float softcap, float *logits, float *probs, hipStream_t s);
 hipError_t dx_pack_gate_up_launch(const uint16_t *gate, const uint16_t *up, uint16_t *packed, long f, long k,
                                   hipStream_t s);
 

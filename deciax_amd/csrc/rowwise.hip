@@ -136,13 +136,16 @@ template <int MAXC>
 __global__ void __launch_bounds__(64 * RO_WAVES)
 readout_kernel(const uint16_t *__restrict__ hidden, const uint16_t *__restrict__ norm_w,
                const uint16_t *__restrict__ table, const int32_t *__restrict__ opt_pos,
-               const int32_t *__restrict__ opt_label, const int32_t *__restrict__ q_off, long hidden_rows, int d,
-               long ld_hidden,
+               const int32_t *__restrict__ opt_label, const int32_t *__restrict__ q_off, int num_options,
+               long hidden_rows, int d, long ld_hidden,
                long vocab, float eps, float softcap, float *__restrict__ logits, float *__restrict__ probs) {
   __shared__ float red[RO_WAVES];
   __shared__ float zs[RO_MAX_LDS];  // the question's logits, when it has at most RO_MAX_LDS options
   const int q = blockIdx.x;
-  const int o0 = q_off[q], o1 = q_off[q + 1];
+  // The offsets come from device memory: clamp the question's range into [0, num_options) so that a
+  // malformed offset array can give wrong answers but never reads or writes outside the option arrays.
+  const int o0 = min(max(q_off[q], 0), num_options);
+  const int o1 = min(max(q_off[q + 1], o0), num_options);
   const bool in_lds = o1 - o0 <= RO_MAX_LDS;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int nch = d / 8;
@@ -253,10 +256,10 @@ struct EmbedRun {
 template <int MAXC>
 struct ReadoutRun {
   static hipError_t run(const uint16_t *hidden, const uint16_t *nw, const uint16_t *table, const int32_t *pos,
-                        const int32_t *lab, const int32_t *q_off, int nq, long hrows, int d, long ldh, long vocab,
-                        float eps, float softcap, float *logits, float *probs, hipStream_t s) {
-    readout_kernel<MAXC><<<dim3(nq), dim3(64 * RO_WAVES), 0, s>>>(hidden, nw, table, pos, lab, q_off, hrows, d, ldh,
-                                                                  vocab, eps, softcap, logits, probs);
+                        const int32_t *lab, const int32_t *q_off, int nq, int nopt, long hrows, int d, long ldh,
+                        long vocab, float eps, float softcap, float *logits, float *probs, hipStream_t s) {
+    readout_kernel<MAXC><<<dim3(nq), dim3(64 * RO_WAVES), 0, s>>>(hidden, nw, table, pos, lab, q_off, nopt, hrows, d,
+                                                                  ldh, vocab, eps, softcap, logits, probs);
     return hipGetLastError();
   }
 };
@@ -288,10 +291,10 @@ hipError_t dx_rope_launch(uint16_t *x, const int32_t *pos, const uint16_t *cos, 
 
 hipError_t dx_readout_launch(const uint16_t *hidden, const uint16_t *norm_w, const uint16_t *table,
                              const int32_t *opt_pos, const int32_t *opt_label, const int32_t *q_off, int nq,
-                             long hidden_rows, int d, long ld_hidden, long vocab, float eps, float softcap,
-                             float *logits, float *probs, hipStream_t s) {
-  return by_chunks<ReadoutRun>(d, hidden, norm_w, table, opt_pos, opt_label, q_off, nq, hidden_rows, d, ld_hidden,
-                               vocab, eps, softcap, logits, probs, s);
+                             int num_options, long hidden_rows, int d, long ld_hidden, long vocab, float eps,
+                             float softcap, float *logits, float *probs, hipStream_t s) {
+  return by_chunks<ReadoutRun>(d, hidden, norm_w, table, opt_pos, opt_label, q_off, nq, num_options, hidden_rows, d,
+                               ld_hidden, vocab, eps, softcap, logits, probs, s);
 }
 
 hipError_t dx_pack_gate_up_launch(const uint16_t *gate, const uint16_t *up, uint16_t *packed, long f, long k,

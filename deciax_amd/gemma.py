@@ -341,7 +341,7 @@ def pack_batch(token_ids: Sequence[Sequence[int]], options: Sequence[Sequence[Se
     order = np.argsort(-np.asarray(lengths), kind="stable")
     by_length = (i32(starts[order]), i32(np.asarray(lengths)[order]), i32(vt_start[order]))
     return PackedBatch(lengths, i32(ids), i32(positions), i32(starts), i32(lengths), i32(vt_start),
-                       int(sum(padded)), i32(vt_col), i32(opt_pos), i32(opt_label), i32(q_off), qpr, opq,
+                       int(sum(padded)), i32(vt_col), i32(opt_pos), i32(opt_label), K.offsets_tensor(q_off, dev), qpr, opq,
                        by_length, tuple(q_off))
 
 

@@ -10,6 +10,7 @@ asynchronously on `torch.cuda.current_stream()`.
 from __future__ import annotations
 
 import ctypes
+import weakref
 from collections.abc import Sequence
 
 import torch
@@ -591,12 +592,28 @@ def flash_attention(qkv: torch.Tensor, mask: torch.Tensor, *, heads: int, window
 # ---------------------------------------------------------------------------- readout
 
 
+# Device offset arrays built by `offsets_tensor`, with the host values they were built from: the
+# readout validates those without reading the device tensor back (which would synchronise the stream).
+_OFFSETS: "weakref.WeakKeyDictionary[torch.Tensor, tuple[int, ...]]" = weakref.WeakKeyDictionary()
+
+
+def offsets_tensor(values: Sequence[int], device: torch.device | str) -> torch.Tensor:
+    """An int32 device copy of question offsets, remembered together with its host values."""
+    host = tuple(int(v) for v in values)
+    t = torch.as_tensor(host, dtype=torch.int32).to(device)
+    _OFFSETS[t] = host
+    return t
+
+
 def readout(hidden: torch.Tensor, norm_w: torch.Tensor, table: torch.Tensor, opt_pos: torch.Tensor,
             opt_label: torch.Tensor, q_offsets: torch.Tensor, *, eps: float, softcap: float = 0.0,
             q_offsets_host: Sequence[int] | None = None) -> tuple[torch.Tensor, torch.Tensor]:
-    """Option logits and per-question probabilities (see dx_readout). `q_offsets` is validated on a
-    host copy: pass `q_offsets_host` (the same values) to avoid reading the device tensor back, which
-    would synchronise the stream."""
+    """Option logits and per-question probabilities (see dx_readout).
+
+    `q_offsets` is validated on the host before the launch. For a tensor made by `offsets_tensor` the
+    values it was built from are used, with no device read; any other tensor is read back (which
+    synchronises the stream). `q_offsets_host`, when given, must equal those values, else ValueError.
+    The kernel also clamps every question's range into the option arrays."""
     _need(hidden, "hidden", BF16, 2)
     _need(norm_w, "norm_w", BF16, 1)
     _need(table, "table", BF16, 2)
@@ -610,9 +627,12 @@ def readout(hidden: torch.Tensor, norm_w: torch.Tensor, table: torch.Tensor, opt
         raise ValueError(f"readout: norm_w and table rows must have {d} entries")
     if q_offsets.shape[0] < 1:
         raise ValueError("readout: q_offsets needs at least one entry")
-    offs = torch.as_tensor(q_offsets_host if q_offsets_host is not None else q_offsets.cpu())
-    if offs.shape != q_offsets.shape:
-        raise ValueError("readout: q_offsets_host must hold the values of q_offsets")
+    known = _OFFSETS.get(q_offsets)
+    if known is None or len(known) != q_offsets.shape[0]:
+        known = tuple(int(v) for v in q_offsets.cpu().tolist())
+    if q_offsets_host is not None and tuple(int(v) for v in q_offsets_host) != known:
+        raise ValueError("readout: q_offsets_host differs from the values of q_offsets")
+    offs = torch.as_tensor(known, dtype=torch.int64)
     if int(offs[0]) != 0 or int(offs[-1]) != nopt or bool((offs[1:] < offs[:-1]).any()):
         raise ValueError("readout: q_offsets must rise monotonically from 0 to the number of options")
     logits = torch.empty(nopt, dtype=F32, device=hidden.device)

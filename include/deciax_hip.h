@@ -332,7 +332,11 @@ int dx_rope(void *x, const int32_t *positions, const void *cos,
  *   logits[o] = softcap > 0 ? softcap * tanh(z / softcap) : z
  *   probs[o]  = softmax over the options of its question (fp32).
  * Positions are clamped into [0, hidden_rows) and labels into [0, vocab) by
- * the kernel; callers validate them first.
+ * the kernel, and each question's range [q_offsets[q], q_offsets[q + 1]) into
+ * [0, num_options), so a malformed device array can give wrong answers but
+ * never touches memory outside the option arrays; callers validate the
+ * offsets first (they must rise from 0 to num_options). num_options above
+ * INT32_MAX is refused with DX_ERR_INVALID.
  * Replaces the marker gather + score + per-question softmax of `_scorer`,
  * src/deciax/models/laya/heads.py:74-91 (gather at marker_pos, masked
  * softmax) and the softmax of `decode`, src/deciax/models/clef/input.py:185-194

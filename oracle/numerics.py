@@ -8,19 +8,27 @@ from contextlib import contextmanager
 import numpy as np
 
 F32 = np.float32
-_ACC = [np.dtype(np.float32)]
+ORDERS = ("blas", "k_tiles")
+K_TILE = 64
+_ACC = [(np.dtype(np.float32), "blas")]
 
 
 def acc_dtype() -> np.dtype:
     """Accumulation dtype of the oracle's contractions (fp32 unless inside `accumulation`)."""
-    return _ACC[-1]
+    return _ACC[-1][0]
 
 
 @contextmanager
-def accumulation(dtype: type) -> Iterator[None]:
+def accumulation(dtype: type, order: str = "blas") -> Iterator[None]:
     """Run the oracle's matrix products in `dtype` (np.float64 gives the exactly-summed value of
-    every contraction, up to the bf16 rounding points, to measure fp32 summation-order noise)."""
-    _ACC.append(np.dtype(dtype))
+    every contraction, up to the bf16 rounding points, to measure fp32 summation-order noise).
+
+    `order` picks one of two valid summation orders of a contraction: "blas" is numpy's BLAS
+    blocking; "k_tiles" sums K in tiles of 64, each tile's partial product added to the running
+    sum in turn, as a tiled GEMM walks K. In fp64 the two agree to fp64 rounding."""
+    if order not in ORDERS:
+        raise ValueError(f"order must be one of {ORDERS}, got {order!r}")
+    _ACC.append((np.dtype(dtype), order))
     try:
         yield
     finally:
@@ -28,9 +36,15 @@ def accumulation(dtype: type) -> Iterator[None]:
 
 
 def matmul(a: np.ndarray, b: np.ndarray) -> np.ndarray:
-    """a @ b accumulated in `acc_dtype()`, returned as fp32."""
-    d = acc_dtype()
-    return (np.asarray(a, d) @ np.asarray(b, d)).astype(F32)
+    """a @ b accumulated in `acc_dtype()` in the current summation order, returned as fp32."""
+    d, order = _ACC[-1]
+    a, b = np.asarray(a, d), np.asarray(b, d)
+    if order == "blas" or a.shape[-1] <= K_TILE:
+        return (a @ b).astype(F32)
+    acc = a[..., :K_TILE] @ b[:K_TILE]
+    for k0 in range(K_TILE, a.shape[-1], K_TILE):
+        acc += a[..., k0:k0 + K_TILE] @ b[k0:k0 + K_TILE]
+    return acc.astype(F32)
 
 
 def bf16(x: np.ndarray) -> np.ndarray:

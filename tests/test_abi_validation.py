@@ -148,3 +148,20 @@ def test_linear_residual_norm_validation() -> None:
     assert lib().dx_linear_residual_norm_counters(0) == 0
     assert lib().dx_linear_residual_norm_counters(70471) == (70471 + 255) // 256
     assert lib().dx_linear_residual_norm_counters(1000) == (1000 + 127) // 128
+
+
+def test_readout_validation() -> None:
+    """dx_readout refuses malformed sizes before any launch; option counts beyond the int32 range of the
+    offsets are refused rather than truncated."""
+    f = ctypes.c_float
+
+    def ro(nq=2, nopt=6, rows=8, d=512, ld=512, vocab=100):
+        return ("dx_readout", P, P, P, P, P, P, nq, nopt, rows, d, ld, vocab, f(1e-6), f(30.0), P, P, NUL)
+
+    name = ro()[0]
+    check(name, _lib.DX_ERR_INVALID, *ro(nopt=-1)[1:])
+    check(name, _lib.DX_ERR_INVALID, *ro(nopt=1 << 31)[1:])
+    check(name, _lib.DX_ERR_INVALID, *ro(rows=0)[1:])
+    check(name, _lib.DX_ERR_INVALID, *ro(ld=256)[1:])
+    check(name, _lib.DX_ERR_UNSUPPORTED, *ro(d=500, ld=504)[1:])
+    check(name, _lib.DX_OK, *ro(nq=0)[1:])

@@ -639,6 +639,40 @@ def test_qkv_rope_matches_unfused(lengths: list[int], hq: int, hkv: int, d: int,
     np.testing.assert_array_equal(bits(vt), bits(vt_ref))
 
 
+def test_readout_malformed_offsets_stay_in_bounds() -> None:
+    """Device offsets that disagree with num_options (past the end, falling, negative) reach the kernel
+    through the C ABI unchecked; the kernel clamps every question's range, so nothing outside the
+    option arrays is written."""
+    import ctypes
+
+    import torch
+
+    from deciax_amd import _lib
+
+    say("readout, malformed device offsets through the C ABI")
+    r = rng(12)
+    rows, d, vocab, nopt, pad = 64, 512, 100, 6, 256
+    hidden = to_dev(bf16_np(r.normal(size=(rows, d))))
+    nw = to_dev(bf16_np(r.normal(size=d) * 0.1))
+    table = to_dev(bf16_np(r.normal(size=(vocab, d)) * 0.02))
+    pos, lab = i32(r.integers(0, rows, nopt)), i32(r.integers(0, vocab, nopt))
+    q_off = i32([0, 2, 1000, -5, 6])          # q0 = [0,2) valid, q1 runs past the end, q2 falls, q3 negative
+    guard_l = torch.full((nopt + 2 * pad,), 7.0, device="cuda")
+    guard_p = torch.full((nopt + 2 * pad,), 7.0, device="cuda")
+    p = lambda t, off=0: ctypes.c_void_p(t.data_ptr() + 4 * off)
+    st = _lib.lib().dx_readout(p(hidden), p(nw), p(table), p(pos), p(lab), p(q_off), 4, nopt, rows, d, d, vocab,
+                               ctypes.c_float(1e-6), ctypes.c_float(30.0), p(guard_l, pad), p(guard_p, pad),
+                               ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    assert st == _lib.DX_OK
+    torch.cuda.synchronize()
+    gl, gp = to_np(guard_l), to_np(guard_p)
+    for g in (gl, gp):
+        assert (g[:pad] == 7.0).all() and (g[pad + nopt:] == 7.0).all()
+    # q3's clamped range [0, 6) overlaps q0's, so only finiteness and range are fixed inside
+    assert np.isfinite(gl[pad:pad + nopt]).all()
+    assert ((gp[pad:pad + nopt] >= 0) & (gp[pad:pad + nopt] <= 1)).all()
+
+
 def test_readout() -> None:
     from deciax_amd import kernels as K
     from oracle.model import readout
@@ -726,6 +760,12 @@ def test_abi_rejects_bad_arguments() -> None:
         K.readout(hidden, nw, hidden, i32([0, 1]), i32([0, 1]), i32([0, 3]), eps=1e-6)
     with pytest.raises(ValueError, match="q_offsets must rise"):
         K.readout(hidden, nw, hidden, i32([0, 1, 2]), i32([0, 1, 2]), i32([0, 2, 1, 3]), eps=1e-6)
+    # host values that differ from the device offsets are refused, registered tensor or not
+    with pytest.raises(ValueError, match="differs from the values"):
+        K.readout(hidden, nw, hidden, i32([0, 1]), i32([0, 1]), K.offsets_tensor([0, 2], "cuda"), eps=1e-6,
+                  q_offsets_host=[0, 1, 2])
+    with pytest.raises(ValueError, match="differs from the values"):
+        K.readout(hidden, nw, hidden, i32([0, 1]), i32([0, 1]), i32([0, 2]), eps=1e-6, q_offsets_host=[0, 1])
     xf = torch.zeros((4, 64), dtype=torch.float32, device="cuda")
     with pytest.raises(ValueError, match="w must be"):
         K.layer_norm_f32(xf, torch.zeros(32, device="cuda"), None, eps=1e-5)
