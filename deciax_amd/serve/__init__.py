@@ -1,5 +1,5 @@
 """`/v1/systemone` HTTP serving on the HIP decision path (`python -m deciax_amd.serve --impl hip`)."""
 
-from deciax_amd.serve.app import Response, Service, make_server, serve
+from deciax_amd.serve.wsgi import DecisionApp, Reply, make_server, serve
 
-__all__ = ["Response", "Service", "make_server", "serve"]
+__all__ = ["DecisionApp", "Reply", "make_server", "serve"]

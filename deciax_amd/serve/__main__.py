@@ -75,7 +75,7 @@ def parse(argv: list[str] | None = None) -> argparse.Namespace:
 def main(argv: list[str] | None = None) -> None:
     args = parse(argv)
     logging.basicConfig(level=args.log_level.upper(), format="%(asctime)s %(levelname)s %(name)s: %(message)s")
-    from deciax_amd.serve.app import serve
+    from deciax_amd.serve.wsgi import serve
 
     serve(args.host, args.port, tuple(args.models), default_model=args.default_model or None,
           api_key=os.environ.get("DECIAX_API_KEY") or None, max_concurrent=args.max_concurrent,

@@ -20,13 +20,13 @@ QUESTIONS = {"sentiment": {"type": "choice", "criteria": {"pos": "positive", "ne
 
 def test_http_service_with_impl_hip() -> None:
     from deciax_amd.serve.__main__ import parse
-    from deciax_amd.serve.app import Service, load_deciders, make_server
-    from deciax_amd.serve.protocol import with_confidence
+    from deciax_amd.serve.contract import with_confidence
+    from deciax_amd.serve.wsgi import DecisionApp, load_deciders, make_server
 
     say("serve --impl hip --model tiny over HTTP")
     args = parse(["--impl", "hip", "--model", "tiny", "--port", "0", "--no-warmup"])
     deciders = load_deciders(tuple(args.models), dtype=args.dtype, impl=args.impl, warmup=True)
-    server = make_server(Service(deciders, "tiny", device="gfx950"), "127.0.0.1", 0)
+    server = make_server(DecisionApp(deciders, "tiny", device="gfx950"), "127.0.0.1", 0)
     thread = threading.Thread(target=server.serve_forever, daemon=True)
     thread.start()
     try:

@@ -1,6 +1,6 @@
-"""The /v1/systemone service and CLI on the CPU, with stand-in deciders (no GPU): routing, status
+"""The /v1/systemone application and CLI on the CPU, with stand-in deciders (no GPU): routing, status
 codes, limits, budgets, model selection and the answer decorations, as the reference's server
-behaves (src/deciax/serve/app.py, src/deciax/protocol/systemone.py)."""
+answers them (src/deciax/serve/app.py, src/deciax/protocol/systemone.py)."""
 
 from __future__ import annotations
 
@@ -11,8 +11,8 @@ from typing import Any
 
 import pytest
 
-from deciax_amd.serve import protocol
-from deciax_amd.serve.app import Service, make_server
+from deciax_amd.serve import contract
+from deciax_amd.serve.wsgi import DecisionApp, make_server
 
 QUESTIONS = {"mood": {"type": "choice", "criteria": {"pos": "positive", "neg": "negative"}},
              "urgent": {"type": "noul"}}
@@ -45,18 +45,18 @@ class FakeDecider:
         return [self._answer(s) for s in states]
 
 
-def post(service: Service, path: str, body: Any, headers: dict[str, str] | None = None):
+def post(service: DecisionApp, path: str, body: Any, headers: dict[str, str] | None = None):
     raw = body if isinstance(body, bytes) else json.dumps(body).encode()
-    return service.handle("POST", path, headers or {}, raw)
+    return service.respond("POST", path, headers or {}, raw)
 
 
 def test_routes_methods_and_health() -> None:
-    s = Service({"tiny": FakeDecider()}, "tiny", api_key="k", device="gfx950")
-    assert s.handle("GET", "/nope", {}, b"").status == 404
-    assert s.handle("GET", "/v1/systemone", {}, b"").status == 405
-    assert s.handle("POST", "/health", {}, b"").status == 405
-    assert s.handle("GET", "/health", {}, b"").payload == {"status": "ok"}
-    full = s.handle("GET", "/health/", {"authorization": "Bearer k"}, b"").payload
+    s = DecisionApp({"tiny": FakeDecider()}, "tiny", api_key="k", device="gfx950")
+    assert s.respond("GET", "/nope", {}, b"").status == 404
+    assert s.respond("GET", "/v1/systemone", {}, b"").status == 405
+    assert s.respond("POST", "/health", {}, b"").status == 405
+    assert s.respond("GET", "/health", {}, b"").payload == {"status": "ok"}
+    full = s.respond("GET", "/health/", {"authorization": "Bearer k"}, b"").payload
     assert full == {"status": "ok", "loaded": ["tiny"], "default_model": "tiny", "device": "gfx950"}
     assert post(s, "/v1/systemone", {"state": "x", "questions": QUESTIONS}).status == 401
     ok = post(s, "/v1/systemone?x=1", {"state": "x", "questions": QUESTIONS}, {"authorization": "Bearer k"})
@@ -64,21 +64,21 @@ def test_routes_methods_and_health() -> None:
 
 
 def test_answers_carry_jev_confidence_or_the_strict_view() -> None:
-    r = post(Service({"tiny": FakeDecider()}, "tiny"), "/v1/systemone", {"state": "x", "questions": QUESTIONS})
+    r = post(DecisionApp({"tiny": FakeDecider()}, "tiny"), "/v1/systemone", {"state": "x", "questions": QUESTIONS})
     mood = r.payload["answers"]["mood"]
     assert mood["x_jev_confidence"] == 0.5  # (0.75 - 1/2) / (1 - 1/2)
     assert "x_jev_confidence" not in r.payload["answers"]["urgent"]
-    strict = post(Service({"tiny": FakeDecider()}, "tiny", jev_strict=True), "/v1/systemone",
+    strict = post(DecisionApp({"tiny": FakeDecider()}, "tiny", jev_strict=True), "/v1/systemone",
                   {"state": "x", "questions": QUESTIONS}).payload
     assert set(strict["answers"]["mood"]) == {"type", "choice", "confidence", "probabilities"}
     assert strict["usage"] == {"input_tokens": 1, "output_tokens": 0}
-    batch = post(Service({"tiny": FakeDecider()}, "tiny"), "/v1/systemone/batch",
+    batch = post(DecisionApp({"tiny": FakeDecider()}, "tiny"), "/v1/systemone/batch",
                  {"states": ["ab", "cde"], "questions": QUESTIONS}).payload
     assert len(batch["results"]) == 2 and batch["total_usage"] == {"input_tokens": 5, "output_tokens": 0}
 
 
 def test_jev_confidence_kats() -> None:
-    c = protocol.confidence
+    c = contract.confidence
     assert c({"type": "choice", "probabilities": {"a": 1.0, "b": 0.0}}) == 1.0
     assert c({"type": "choice", "probabilities": {"a": 0.5, "b": 0.5}}) == 0.0
     assert c({"type": "choice", "probabilities": {"a": 1.0}}) == 1.0
@@ -109,22 +109,22 @@ def test_jev_confidence_kats() -> None:
     ({"state": "x", "questions": QUESTIONS, "model": "../weights"}, 422),
 ])
 def test_client_errors(body: Any, status: int) -> None:
-    r = post(Service({"tiny": FakeDecider()}, "tiny"), "/v1/systemone", body)
+    r = post(DecisionApp({"tiny": FakeDecider()}, "tiny"), "/v1/systemone", body)
     assert r.status == status, r.payload
     assert isinstance(r.payload["detail"], str)
 
 
 def test_batch_limits_and_body_size() -> None:
-    s = Service({"tiny": FakeDecider()}, "tiny")
+    s = DecisionApp({"tiny": FakeDecider()}, "tiny")
     assert post(s, "/v1/systemone/batch", {"states": [], "questions": QUESTIONS}).status == 400
     assert post(s, "/v1/systemone/batch", {"states": ["x"] * 65, "questions": QUESTIONS}).status == 413
     assert post(s, "/v1/systemone/batch", {"states": ["x"], "questions": QUESTIONS, "batch_size": 4}).status == 422
-    assert post(s, "/v1/systemone", b" " * (protocol.MAX_BODY_BYTES + 1)).status == 413
+    assert post(s, "/v1/systemone", b" " * (contract.MAX_BODY_BYTES + 1)).status == 413
 
 
 def test_budgets_and_model_selection() -> None:
     a, b = FakeDecider("tiny"), FakeDecider("other")
-    s = Service({"tiny": a, "other": b}, "tiny")
+    s = DecisionApp({"tiny": a, "other": b}, "tiny")
     assert post(s, "/v1/systemone", {"state": "x", "questions": QUESTIONS, "max_len": 100}).status == 200
     assert a.calls[-1] == {"max_len": 100}
     post(s, "/v1/systemone", {"state": "x", "questions": QUESTIONS, "model": "other"})
@@ -134,10 +134,10 @@ def test_budgets_and_model_selection() -> None:
 
 
 def test_model_errors_map_to_422_and_500() -> None:
-    bad = Service({"tiny": FakeDecider(fail=ValueError("schema requires 9999 tokens"))}, "tiny")
+    bad = DecisionApp({"tiny": FakeDecider(fail=ValueError("schema requires 9999 tokens"))}, "tiny")
     r = post(bad, "/v1/systemone", {"state": "x", "questions": QUESTIONS})
     assert r.status == 422 and "9999" in r.payload["detail"]
-    broken = Service({"tiny": FakeDecider(fail=RuntimeError("device lost"))}, "tiny")
+    broken = DecisionApp({"tiny": FakeDecider(fail=RuntimeError("device lost"))}, "tiny")
     r = post(broken, "/v1/systemone", {"state": "x", "questions": QUESTIONS})
     assert r.status == 500 and r.payload == {"detail": "inference failed"}
 
@@ -151,7 +151,7 @@ def test_admission_limit_returns_503() -> None:
             gate.wait(10)
             return super().decide(state, questions, **budgets)
 
-    s = Service({"tiny": Slow()}, "tiny", max_concurrent=1)
+    s = DecisionApp({"tiny": Slow()}, "tiny", max_concurrent=1)
     t = threading.Thread(target=post, args=(s, "/v1/systemone", {"state": "x", "questions": QUESTIONS}))
     t.start()
     assert entered.wait(10)
@@ -162,7 +162,7 @@ def test_admission_limit_returns_503() -> None:
 
 
 def test_http_round_trip() -> None:
-    server = make_server(Service({"tiny": FakeDecider()}, "tiny"), "127.0.0.1", 0)
+    server = make_server(DecisionApp({"tiny": FakeDecider()}, "tiny"), "127.0.0.1", 0)
     thread = threading.Thread(target=server.serve_forever, daemon=True)
     thread.start()
     try:
@@ -173,11 +173,20 @@ def test_http_round_trip() -> None:
         r = conn.getresponse()
         body = json.loads(r.read())
         assert r.status == 200 and body["answers"]["mood"]["choice"] == "pos"
-        conn.putrequest("POST", "/v1/systemone")
-        conn.endheaders()  # no Content-Length
+        for length, status in ((None, 411), ("-5", 400), ("abc", 400), (str(contract.MAX_BODY_BYTES + 1), 413)):
+            conn.close()
+            conn.putrequest("POST", "/v1/systemone")
+            if length is not None:
+                conn.putheader("Content-Length", length)
+            conn.endheaders()  # no body follows: a refused body is never read
+            r = conn.getresponse()
+            assert r.status == status, (length, r.status)
+            assert isinstance(json.loads(r.read())["detail"], str)
+        conn.close()
+        conn.request("GET", "/health")
         r = conn.getresponse()
-        assert r.status == 411
-        r.read()
+        assert r.status == 200 and json.loads(r.read()) == {"status": "ok", "loaded": ["tiny"],
+                                                            "default_model": "tiny", "device": "unknown"}
         conn.close()
     finally:
         server.shutdown()
@@ -214,3 +223,38 @@ def test_cli_without_a_gfx950_device_refuses_hip() -> None:
         pytest.skip("a GPU is visible; the GPU test serves for real")
     with pytest.raises(ValueError, match="gfx950"):
         main(["--impl", "hip", "--model", "tiny", "--no-warmup", "--port", "0"])
+
+
+def test_refusal_order_follows_the_contract() -> None:
+    """Where a request breaks several rules, the contract names the one reported."""
+    s = DecisionApp({"tiny": FakeDecider()}, "tiny")
+    many = {f"q{i}": {"type": "choice", "criteria": {str(j): "o" for j in range(101)}} for i in range(65)}
+    # more than 64 questions is reported before any per-question cap
+    assert post(s, "/v1/systemone", {"state": "x", "questions": many}).payload["detail"].startswith("too many questions")
+    # a score question over its level cap is reported before its null level
+    over = {"s": {"type": "score", "criteria": [None] * 33}}
+    assert post(s, "/v1/systemone", {"state": "x", "questions": over}).status == 413
+    # limits come before refused fields, refused fields before the encoding check, that before budgets
+    r = post(s, "/v1/systemone", {"state": "x" * 50001, "questions": QUESTIONS, "hooks": 1})
+    assert r.status == 413
+    r = post(s, "/v1/systemone", {"state": "\ud800", "questions": QUESTIONS, "lang": "en", "max_len": 0})
+    assert r.status == 422 and "lang" in r.payload["detail"]
+    r = post(s, "/v1/systemone", {"state": "\ud800", "questions": QUESTIONS, "max_len": 0})
+    assert r.status == 400
+    # a surrogate in a key is caught as well as in a value
+    r = post(s, "/v1/systemone", {"state": {"\udfff": 1}, "questions": QUESTIONS})
+    assert r.status == 400 and r.payload["detail"] == contract.SURROGATE_DETAIL
+    # too many options across questions, each within its own cap
+    spread = {f"c{i}": {"type": "choice", "criteria": [str(j) for j in range(90)]} for i in range(6)}
+    r = post(s, "/v1/systemone", {"state": "x", "questions": spread})
+    assert r.status == 413 and "across questions (540 > 512)" in r.payload["detail"]
+
+
+def test_strict_view_and_confidence_tables_cover_every_answer_type() -> None:
+    assert set(contract.STRICT_FIELDS) == {"choice", "score", "noul"}
+    assert set(contract.CONFIDENCE) == {"choice", "score"}
+    # score levels are ordered by their integer key, not by insertion order
+    assert contract.confidence({"type": "score", "probabilities": {"2": 0.0, "0": 0.0, "1": 1.0}}) == 1.0
+    assert contract.confidence({"type": "score", "probabilities": {"a": 0.5, "b": 0.5}}) is None
+    # zero total mass counts as uniform
+    assert contract.confidence({"type": "choice", "probabilities": {"a": 0.0, "b": 0.0}}) == 0.0
