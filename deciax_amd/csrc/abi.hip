@@ -170,17 +170,17 @@ int attn_prefill(const void *q, const void *k, const void *v, const uint8_t *key
   const int64_t vec = dtype == DX_BF16 ? 8 : 4;
   REQUIRE(v_row_stride % vec == 0 && v_row_stride >= (int64_t)num_kv_heads * head_dim,
           "attention: bad v row stride %ld", (long)v_row_stride);
+  // the matrix-core fp32 kernel (head_dim 64 and 128) reads a 32-key block of K or V through a buffer
+  // resource with 32-bit byte offsets; the head_dim 256 kernel addresses with 64-bit pointers
+  if (dtype == DX_F32)
+    SUPPORTED(head_dim > 128 || (k_row_stride < (INT64_C(1) << 24) && v_row_stride < (INT64_C(1) << 24)),
+              "attention: fp32 k / v row strides of 2^24 elements or more are not supported at head_dim %d",
+              head_dim);
   if (num_seqs == 0 || max_seq_len == 0) return DX_OK;
   AttnArgs a{q, k, v, out, seq_start, seq_len, nullptr, num_seqs, max_seq_len, num_q_heads, num_kv_heads, head_dim,
              q_row_stride, k_row_stride, v_row_stride, out_row_stride, 0, scale, softcap, window, causal ? 1 : 0};
   a.key_mask = key_mask;
-  if (dtype == DX_F32) {
-    // the matrix-core fp32 kernel reads a 32-key block of K or V through a buffer resource with 32-bit
-    // byte offsets
-    SUPPORTED(k_row_stride < (INT64_C(1) << 24) && v_row_stride < (INT64_C(1) << 24),
-              "attention: fp32 k / v row strides of 2^24 elements or more are not supported");
-    return check_launch(dx_attn_f32(a, as_stream(stream)), "attention fp32 launch");
-  }
+  if (dtype == DX_F32) return check_launch(dx_attn_f32(a, as_stream(stream)), "attention fp32 launch");
 
   const int64_t seq_stride = align_up(max_seq_len, 64);
   const int64_t vt_ld = seq_stride * num_seqs;

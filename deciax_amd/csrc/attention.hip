@@ -23,8 +23,13 @@
 // Softmax: with logit soft-capping (Gemma-2, cap <= 56) every capped score
 // lies in (-cap, cap), so p = exp(t - cap/2) is computed with a fixed shift:
 // no running max, no rescaling of the O accumulator, no cross-lane max.
-// t - cap/2 = cap/2 - 2 cap / (1 + e^{2x}), x = scale * s / cap, hence
-//   p = exp2(c3 + c2 / (1 + exp2(c1 s))).
+// t - cap/2 = cap/2 - 2 cap / (1 + e^{2x}), x = scale * s / cap, hence in log2
+// units c3 + c2 / (1 + exp2(c1 s)) with c1 = 2 log2(e) scale / cap,
+// c2 = -2 cap log2(e), c3 = cap log2(e) / 2. The kernel multiplies q by c1 as it
+// loads it (one bf16 rounding of c1 q), so the MFMA yields c1 s directly, and
+// folds c2 into the reciprocal:
+//   p = exp2(c3 + 1 / fma(exp2(c1 s), 1/c2, 1/c2)),
+// three transcendentals and two ordinary VALU operations per score.
 // p stays within [e^{-3cap/2}, e^{cap/2}] — normal fp32 and bf16 numbers for
 // cap <= 56 — and softmax is invariant to the shift. Without soft-capping (or
 // for larger caps) the kernel keeps the usual running max in log2 units.
@@ -190,6 +195,17 @@ attn_bf16_kernel(const uint16_t *__restrict__ Q, const uint16_t *__restrict__ K,
 #pragma unroll
     for (int ks = 0; ks < NKS; ++ks) qf[ks] = as_bf16x8(*reinterpret_cast<const u32x4 *>(qp + ks * 16));
   }
+  if constexpr (MODE == MODE_FIXED) {
+    // q <- bf16(c1 q): the QK^T MFMAs then give the exponent c1 s of the fixed-shift softmax below
+    const float c1 = 2.f * LOG2E * scale / softcap;
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks) {
+      u32x4 w = __builtin_bit_cast(u32x4, qf[ks]);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) w[i] = pack_bf2(lo_bf(w[i]) * c1, hi_bf(w[i]) * c1);
+      qf[ks] = as_bf16x8(w);
+    }
+  }
 
   const int qlast = min(q0 + BQ, len) - 1;
   int klo, khi;
@@ -242,8 +258,7 @@ attn_bf16_kernel(const uint16_t *__restrict__ Q, const uint16_t *__restrict__ K,
   float lsum = 0.f;
   float mrun = NEG_BIG;
 
-  const float c1 = 2.f * LOG2E * scale / softcap;
-  const float c2 = -2.f * LOG2E * softcap;
+  const float c2inv = 1.f / (-2.f * LOG2E * softcap);
   const float c3 = 0.5f * LOG2E * softcap;
 
   // Which 32-key blocks this wave's rows see: active = some key visible, masked = some key hidden.
@@ -303,8 +318,8 @@ attn_bf16_kernel(const uint16_t *__restrict__ Q, const uint16_t *__restrict__ K,
     if constexpr (MODE == MODE_FIXED) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const float e = fast_exp2(s[r] * c1);
-        float p = fast_exp2(c3 + c2 * fast_rcp(1.f + e));
+        const float e = fast_exp2(s[r]);  // s[r] = c1 * score: q was scaled by c1 at load
+        float p = fast_exp2(fast_rcp(__builtin_fmaf(e, c2inv, c2inv)) + c3);
         if constexpr (M) p = keep(r) ? p : 0.f;
         s[r] = p;
         lsum += p;

@@ -594,15 +594,27 @@ def flash_attention(qkv: torch.Tensor, mask: torch.Tensor, *, heads: int, window
 
 # Device offset arrays built by `offsets_tensor`, with the host values they were built from: the
 # readout validates those without reading the device tensor back (which would synchronise the stream).
-_OFFSETS: "weakref.WeakKeyDictionary[torch.Tensor, tuple[int, ...]]" = weakref.WeakKeyDictionary()
+# Keyed by id(); the weak reference confirms the entry still belongs to that tensor, and a finalizer
+# drops it with the tensor.
+_OFFSETS: dict[int, tuple[weakref.ref, tuple[int, ...]]] = {}
 
 
 def offsets_tensor(values: Sequence[int], device: torch.device | str) -> torch.Tensor:
     """An int32 device copy of question offsets, remembered together with its host values."""
     host = tuple(int(v) for v in values)
     t = torch.as_tensor(host, dtype=torch.int32).to(device)
-    _OFFSETS[t] = host
+    key = id(t)
+    _OFFSETS[key] = (weakref.ref(t), host)
+    weakref.finalize(t, _OFFSETS.pop, key, None)
     return t
+
+
+def known_offsets(t: torch.Tensor) -> tuple[int, ...] | None:
+    """The host values `t` was built from by `offsets_tensor`, or None for any other tensor."""
+    entry = _OFFSETS.get(id(t))
+    if entry is None or entry[0]() is not t or len(entry[1]) != t.shape[0]:
+        return None
+    return entry[1]
 
 
 def readout(hidden: torch.Tensor, norm_w: torch.Tensor, table: torch.Tensor, opt_pos: torch.Tensor,
@@ -627,8 +639,8 @@ def readout(hidden: torch.Tensor, norm_w: torch.Tensor, table: torch.Tensor, opt
         raise ValueError(f"readout: norm_w and table rows must have {d} entries")
     if q_offsets.shape[0] < 1:
         raise ValueError("readout: q_offsets needs at least one entry")
-    known = _OFFSETS.get(q_offsets)
-    if known is None or len(known) != q_offsets.shape[0]:
+    known = known_offsets(q_offsets)
+    if known is None:
         known = tuple(int(v) for v in q_offsets.cpu().tolist())
     if q_offsets_host is not None and tuple(int(v) for v in q_offsets_host) != known:
         raise ValueError("readout: q_offsets_host differs from the values of q_offsets")

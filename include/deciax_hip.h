@@ -81,8 +81,9 @@ int dx_device_arch(int device, char *buf, int buf_len);
  * offsets: max_seq_len * k_row_stride * 2 and ((head_dim - 1) * vt_ld +
  * max_seq_len rounded up to 64) * 2 must stay below 2^31 (DX_ERR_UNSUPPORTED
  * otherwise; vt_ld is the V^T leading dimension, here max_seq_len rounded up
- * to 64 times num_seqs). The fp32 path reads 32-key blocks with 32-bit byte
- * offsets: k_row_stride and v_row_stride must stay below 2^24 elements. */
+ * to 64 times num_seqs). At head_dim 64 and 128 the fp32 path reads 32-key
+ * blocks with 32-bit byte offsets: k_row_stride and v_row_stride must stay
+ * below 2^24 elements there (head_dim 256 has no such limit). */
 int dx_attn_prefill(const void *q, const void *k, const void *v, void *out,
                     const int32_t *seq_start, const int32_t *seq_len,
                     int32_t num_seqs, int32_t max_seq_len, int32_t num_q_heads,

@@ -17,7 +17,11 @@ few layers is of the order of 1e-3 in option probabilities, so the oracle
 restates the flash form exactly as the GPU path evaluates it: the reference
 point m is the row maximum, except for soft-capped scores, where every score
 lies in (-cap, cap) and m is the fixed bound cap / 2 (the kernel needs no
-running max then). In fp32 the two forms coincide up to fp32 rounding.
+running max then). With that fixed shift the bf16 kernel also multiplies the
+query by c1 = 2 log2(e) scale / cap as it loads it, one more bf16 rounding, so
+that its QK^T products are already the exponent's argument; the flash form in
+bf16 mode scores with bf16(c1 q) as well. In fp32 the two forms coincide up to
+fp32 rounding.
 
 Gemma-2 additions the reference has no code for:
   * logit soft-capping after scaling and before the mask,
@@ -37,6 +41,7 @@ from oracle.numerics import F32, acc_dtype, matmul, maybe, softcap
 
 MASK_FILL = F32(-1e30)
 BLOCK = 128
+LOG2E = 1.4426950408889634
 
 
 def visible(qpos: np.ndarray, kpos: np.ndarray, length: int, window: int, causal: bool) -> np.ndarray:
@@ -76,13 +81,18 @@ def attention_seq(q: np.ndarray, k: np.ndarray, v: np.ndarray, *, scale: float, 
     kpos = np.arange(nk)
     kmask = np.ones(nk, bool) if key_mask is None else np.asarray(key_mask, bool)
     fixed = 0.0 < softcap_value <= FIXED_SHIFT_MAX_CAP
+    fold = fixed and bf16 and rounding == "flash"
+    c1 = F32(2.0 * LOG2E * scale / softcap_value) if fold else F32(1.0)
     for b0 in range(0, len(qpos), BLOCK):
         rows = qpos[b0:b0 + BLOCK]
         ok = visible(rows, kpos, nk, window, causal) & kmask[None, :]
         empty = ~ok.any(axis=1, keepdims=True)  # every score MASK_FILL: softmax is uniform over all keys
         for h in range(hq):
             g = h // group
-            scores = matmul(q[rows, h, :], k[:, g, :].T) * F32(scale)
+            if fold:  # the kernel's pre-scaled query: scores from bf16(c1 q), then back to scale units
+                scores = matmul(maybe(q[rows, h, :] * c1, True), k[:, g, :].T) * F32(scale / c1)
+            else:
+                scores = matmul(q[rows, h, :], k[:, g, :].T) * F32(scale)
             scores = softcap(scores, softcap_value)
             scores = np.where(ok, scores, MASK_FILL)
             vg = v[:, g, :].astype(F32)

@@ -8,7 +8,7 @@ from contextlib import contextmanager
 import numpy as np
 
 F32 = np.float32
-ORDERS = ("blas", "k_tiles")
+ORDERS = ("blas", "k_tiles", "k_tiles_reversed")
 K_TILE = 64
 _ACC = [(np.dtype(np.float32), "blas")]
 
@@ -23,9 +23,10 @@ def accumulation(dtype: type, order: str = "blas") -> Iterator[None]:
     """Run the oracle's matrix products in `dtype` (np.float64 gives the exactly-summed value of
     every contraction, up to the bf16 rounding points, to measure fp32 summation-order noise).
 
-    `order` picks one of two valid summation orders of a contraction: "blas" is numpy's BLAS
+    `order` picks one of three valid summation orders of a contraction: "blas" is numpy's BLAS
     blocking; "k_tiles" sums K in tiles of 64, each tile's partial product added to the running
-    sum in turn, as a tiled GEMM walks K. In fp64 the two agree to fp64 rounding."""
+    sum in turn, as a tiled GEMM walks K; "k_tiles_reversed" walks the same tiles from the last.
+    In fp64 they agree to fp64 rounding."""
     if order not in ORDERS:
         raise ValueError(f"order must be one of {ORDERS}, got {order!r}")
     _ACC.append((np.dtype(dtype), order))
@@ -41,8 +42,11 @@ def matmul(a: np.ndarray, b: np.ndarray) -> np.ndarray:
     a, b = np.asarray(a, d), np.asarray(b, d)
     if order == "blas" or a.shape[-1] <= K_TILE:
         return (a @ b).astype(F32)
-    acc = a[..., :K_TILE] @ b[:K_TILE]
-    for k0 in range(K_TILE, a.shape[-1], K_TILE):
+    starts = list(range(0, a.shape[-1], K_TILE))
+    if order == "k_tiles_reversed":
+        starts.reverse()
+    acc = a[..., starts[0]:starts[0] + K_TILE] @ b[starts[0]:starts[0] + K_TILE]
+    for k0 in starts[1:]:
         acc += a[..., k0:k0 + K_TILE] @ b[k0:k0 + K_TILE]
     return acc.astype(F32)
 

@@ -12,15 +12,26 @@ memory so that the 42- and 46-layer shapes fit:
    probabilities within 1e-3 absolute, with the same argmax wherever the oracle's top-2 gap exceeds
    1e-3.
 3. End to end. The GPU probabilities are compared with the oracle run freely from the embedding
-   (exact sums: the truth), and the fp32 oracle's own distance from that truth is measured beside
-   them. Through bf16 rounding points the two drift apart layer by layer: each 1-ulp flip of a
-   rounded output, caused by a different fp32 summation order, perturbs every output of the next
-   contraction in that row. At the 9B and 27B shapes with random-init weights the fp32 oracle
-   itself ends 2e-2 from the truth after 42 / 46 layers (it is 4e-3 after 3 layers). So the
-   end-to-end distance is recorded rather than held to 1e-3. It must stay below a gross-error
-   guard of 5e-2, and the argmax must agree wherever the truth's top-2 gap exceeds twice the fp32
-   oracle's drift. The reference itself measured 3.0e-3 between two of its own paths
+   with exact sums (the truth). Beside them run three fp32 oracles that differ only in the summation
+   order of their contractions (numpy's BLAS blocking, and K in tiles of 64 walked forwards and
+   backwards as a tiled GEMM walks it); for the "normalized" rounding point a fourth runs the
+   kernel's flash rounding point. These and the truth are all valid implementations of the path; the
+   largest distance between any two of them is the floor: how far apart valid implementations land,
+   estimated from several pairs so that one lucky pair does not set it. Through the
+   bf16 rounding points each 1-ulp flip of a rounded output perturbs every output of the next
+   contraction in its row, and the flips multiply from layer to layer: at the 9B and 27B shapes with
+   random-init weights the floor is about 2e-2 after 42 / 46 layers (4e-3 after 3). The GPU must stay
+   within max(1e-3, 1.5 x floor), so that a path whose drift doubled fails, and its argmax must match
+   the truth wherever the truth's top-2 gap exceeds twice the floor. The GPU's own distance is one
+   more draw of the same chaotic process, so the factor leaves room for one unlucky draw: one measured
+   case (27B shape, 2 layers, window 128) drew 1.29 x the largest of six pairwise distances. The reference itself measured 3.0e-3 between two of its own paths
    (docs/clef-tp.md:48) and accepts 0.02 in bf16 (tests/laya/test_parity.py:21).
+4. Optionally, the same forward read out under final-norm weights scaled by a readout temperature
+   tau: (1 + w) -> tau (1 + w). The final norm enters only the readout, so this is exactly the
+   forward with those weights; every layer runs as in the random-init regime, and the option logits
+   shrink by tau, and with them the floor. At tau = 0.01 the floor is below 3e-4 at full depth, and
+   there the GPU is held to the 1e-3 bar itself, with identical argmax wherever the truth's top-2
+   gap exceeds 2e-3.
 
 Each check appends one line to `RECORDS`; conftest prints them at the end of the pytest run.
 """
@@ -37,7 +48,9 @@ from oracle.numerics import F32, accumulation, bf16
 LAYER_MAX_REL = 2e-2      # bf16 output tolerance, of the layer's largest |x|
 LAYER_REL_L2 = 1e-2
 READOUT_ABS = 1e-3        # option probabilities from the GPU's final hidden state
-E2E_GUARD = 5e-2          # gross-error guard on the free-running forward (see module docstring)
+E2E_BAR = 1e-3            # the target's end-to-end bar on option probabilities
+FLOOR_FACTOR = 1.5        # end to end: the GPU within max(E2E_BAR, FLOOR_FACTOR x the fp32 floor)
+TAU_GAP = 2e-3            # in the tau regime, argmax must match wherever truth's top-2 gap exceeds this
 
 RECORDS: list[str] = []
 
@@ -53,12 +66,18 @@ class ForwardParity:
     e2e_fp32_floor: float
     argmax_agree: int
     questions: int
+    tau: dict[float, tuple[float, float, int, int]] | None = None  # tau -> (e2e, floor, agree, checked)
 
     def line(self) -> str:
-        return (f"{self.name}: {self.layers} layers; per layer max relL2 {self.worst_layer_rel_l2:.2e}, "
+        text = (f"{self.name}: {self.layers} layers; per layer max relL2 {self.worst_layer_rel_l2:.2e}, "
                 f"max |dx|/max|x| {self.worst_layer_max_rel:.2e}; readout |dp| {self.readout_err:.2e}; "
-                f"end to end |p - truth| {self.e2e_err:.2e} (fp32 oracle {self.e2e_fp32_floor:.2e}); "
+                f"end to end |p - truth| {self.e2e_err:.2e} (fp32 floor {self.e2e_fp32_floor:.2e}, "
+                f"bound {max(E2E_BAR, FLOOR_FACTOR * self.e2e_fp32_floor):.2e}); "
                 f"argmax {self.argmax_agree}/{self.questions}")
+        for t, (e2e, floor, agree, checked) in (self.tau or {}).items():
+            text += (f"; tau {t}: |p - truth| {e2e:.2e} (bar {E2E_BAR:.0e}, fp32 floor {floor:.2e}), "
+                     f"argmax {agree}/{checked} with gap > {TAU_GAP:.0e}")
+        return text
 
 
 def shape_of(config) -> om.Shape:
@@ -76,23 +95,32 @@ def _top2_gap(p: np.ndarray) -> float:
     return float(top[0] - top[1])
 
 
-def check_forward(name: str, weights, batch, rounding: str = "flash") -> ForwardParity:
+def check_forward(name: str, weights, batch, rounding: str = "flash",
+                  readout_temperatures: tuple[float, ...] = ()) -> ForwardParity:
     """Run the HIP forward on `batch` (weights built with keep_unpacked=True) and check it against
     the oracle as the module docstring describes. Returns the measured numbers.
 
     `rounding` is where the oracle's attention rounds its weights to bf16: "flash" rounds the
     unnormalised p and divides by the fp32 sum, as the kernel does; "normalized" rounds the
-    normalised weights, the reference's point (src/deciax/kernels/attention/blocked.py:27)."""
+    normalised weights, the reference's point (src/deciax/kernels/attention/blocked.py:27).
+    `readout_temperatures` adds step 4 of the module docstring for each tau given."""
     import torch
 
     from deciax_amd import gemma
+    from deciax_amd import kernels as K
 
     cfg = weights.config
     s = shape_of(cfg)
     rows = batch.rows
     xs: list[np.ndarray] = []
-    logits, probs = gemma.forward(weights, batch,
-                                  on_layer=lambda i, x: xs.append(x[:rows].float().cpu().numpy()))
+    final: list[torch.Tensor] = []
+
+    def keep(i: int, x: torch.Tensor) -> None:
+        xs.append(x[:rows].float().cpu().numpy())
+        if i == cfg.layers:
+            final.append(x[:rows].clone())
+
+    logits, probs = gemma.forward(weights, batch, on_layer=keep)
     torch.cuda.synchronize()
     z_gpu, p_gpu = logits.cpu().numpy(), probs.cpu().numpy()
     assert np.isfinite(p_gpu).all() and np.isfinite(z_gpu).all()
@@ -113,19 +141,25 @@ def check_forward(name: str, weights, batch, rounding: str = "flash") -> Forward
     x0 = bf16(table[remap[ids]] * F32(om.embed_scale(s.hidden)))
     assert np.array_equal(x0, xs[0]), f"{name}: embedding differs from the oracle"
 
-    def readout(x: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
-        return om.readout(x, final_norm, table, opt_pos, remap[opt_label], q_off, eps=s.eps, cap=s.final_softcap)
+    def readout(x: np.ndarray, norm: np.ndarray = final_norm) -> tuple[np.ndarray, np.ndarray]:
+        return om.readout(x, norm, table, opt_pos, remap[opt_label], q_off, eps=s.eps, cap=s.final_softcap)
 
-    truth, free32 = x0.copy(), x0.copy()
+    # the fp32 oracles: (summation order, attention rounding point); the GPU rounds at the flash point
+    variants = [("blas", rounding), ("k_tiles", rounding), ("k_tiles_reversed", rounding)]
+    if rounding != "flash":
+        variants.append(("blas", "flash"))
+    truth = x0.copy()
+    free32 = [x0.copy() for _ in variants]
     worst_l2 = worst_max = 0.0
     for i in range(cfg.layers):
         p = weights.numpy_layer(i)
-        args = (p, s, i, starts, batch.lengths, pos, cos, sin, True, rounding)
+        args = (p, s, i, starts, batch.lengths, pos, cos, sin, True)
         with accumulation(np.float64):
-            forced = om.layer(xs[i], *args)
-            truth = om.layer(truth, *args)
-        with accumulation(np.float32):
-            free32 = om.layer(free32, *args)
+            forced = om.layer(xs[i], *args, rounding)
+            truth = om.layer(truth, *args, rounding)
+        for j, (order, point) in enumerate(variants):
+            with accumulation(np.float32, order):
+                free32[j] = om.layer(free32[j], *args, point)
         d = xs[i + 1] - forced
         rel_l2 = float(np.linalg.norm(d) / max(np.linalg.norm(forced), 1e-30))
         max_rel = float(np.abs(d).max() / max(np.abs(forced).max(), 1e-30))
@@ -137,23 +171,49 @@ def check_forward(name: str, weights, batch, rounding: str = "flash") -> Forward
     z_ro, p_ro = readout(xs[-1])
     readout_err = float(np.abs(p_gpu - p_ro).max()) if len(p_gpu) else 0.0
     assert readout_err <= READOUT_ABS, f"{name}: readout differs by {readout_err:.2e}"
-    _, p_truth = readout(truth)
-    _, p_free32 = readout(free32)
-    e2e = float(np.abs(p_gpu - p_truth).max()) if len(p_gpu) else 0.0
-    floor = float(np.abs(p_free32 - p_truth).max()) if len(p_gpu) else 0.0
-    agree, questions = 0, 0
-    for a, b in zip(q_off[:-1], q_off[1:]):
-        if b - a < 2:
-            continue
-        questions += 1
-        same = int(np.argmax(p_gpu[a:b]) == np.argmax(p_truth[a:b]))
-        agree += same
-        if _top2_gap(p_ro[a:b]) > READOUT_ABS:
-            assert np.argmax(p_gpu[a:b]) == np.argmax(p_ro[a:b]), f"{name}: readout argmax differs"
-        if _top2_gap(p_truth[a:b]) > 2 * floor:
+    def end_to_end(p_dev: np.ndarray, norm: np.ndarray, gap: float | None) -> tuple[float, float, int, int]:
+        """(max |p - truth|, fp32 floor, argmax agreements, questions checked); asserts argmax identity
+        wherever truth's top-2 gap exceeds `gap` (twice the floor when None)."""
+        if not len(p_dev):
+            return 0.0, 0.0, 0, 0
+        p_truth = readout(truth, norm)[1]
+        err = float(np.abs(p_dev - p_truth).max())
+        valid = [p_truth] + [readout(f, norm)[1] for f in free32]
+        floor = max(float(np.abs(a - b).max()) for i, a in enumerate(valid) for b in valid[i + 1:])
+        bar = 2 * floor if gap is None else gap
+        agree = checked = 0
+        for a, b in zip(q_off[:-1], q_off[1:]):
+            if b - a < 2 or _top2_gap(p_truth[a:b]) <= bar:
+                continue
+            checked += 1
+            same = np.argmax(p_dev[a:b]) == np.argmax(p_truth[a:b])
+            agree += int(same)
             assert same, f"{name}: argmax differs from the truth with top-2 gap {_top2_gap(p_truth[a:b]):.2e}"
-    result = ForwardParity(name, cfg.layers, worst_l2, worst_max, readout_err, e2e, floor, agree, questions)
+        return err, floor, agree, checked
+
+    for a, b in zip(q_off[:-1], q_off[1:]):
+        if b - a >= 2 and _top2_gap(p_ro[a:b]) > READOUT_ABS:
+            assert np.argmax(p_gpu[a:b]) == np.argmax(p_ro[a:b]), f"{name}: readout argmax differs"
+    e2e, floor, _, _ = end_to_end(p_gpu, final_norm, None)
+    questions = sum(1 for a, b in zip(q_off[:-1], q_off[1:]) if b - a >= 2)
+    p_truth = readout(truth)[1] if len(p_gpu) else p_gpu
+    agree = sum(int(np.argmax(p_gpu[a:b]) == np.argmax(p_truth[a:b])) for a, b in zip(q_off[:-1], q_off[1:])
+                if b - a >= 2)
+
+    tau_results: dict[float, tuple[float, float, int, int]] = {}
+    for t in readout_temperatures:
+        norm_t = bf16(F32(t) * (F32(1.0) + final_norm) - F32(1.0))
+        norm_dev = torch.from_numpy(norm_t).to(device=final[0].device, dtype=torch.bfloat16)
+        _, p_t = K.readout(final[0], norm_dev, weights.embed, batch.opt_pos, batch.opt_label, batch.q_offsets,
+                           eps=cfg.eps, softcap=cfg.final_softcap)
+        tau_results[t] = end_to_end(p_t.cpu().numpy(), norm_t, TAU_GAP)
+
+    result = ForwardParity(name, cfg.layers, worst_l2, worst_max, readout_err, e2e, floor, agree, questions,
+                           tau_results or None)
     RECORDS.append(result.line())
     print(result.line(), flush=True)
-    assert e2e <= E2E_GUARD, f"{name}: end-to-end error {e2e:.2e} beyond the gross-error guard"
+    bound = max(E2E_BAR, FLOOR_FACTOR * floor)
+    assert e2e <= bound, f"{name}: end-to-end error {e2e:.2e} beyond {FLOOR_FACTOR} x the fp32 floor {floor:.2e}"
+    for t, (err, t_floor, _, _) in tau_results.items():
+        assert err <= E2E_BAR, f"{name}: at readout temperature {t} the end-to-end error is {err:.2e}"
     return result

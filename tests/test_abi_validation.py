@@ -114,6 +114,14 @@ def test_attention_32bit_ranges_refused() -> None:
     fp32 = status("dx_attn_prefill", P, P, P, P, P, P, 1, 64, 8, 4, 128, 1024, 1 << 24, 512, 1024,
                   f(0.088), f(0.0), 0, 1, _lib.DX_F32, NUL, 0, NUL)
     assert fp32 == _lib.DX_ERR_UNSUPPORTED and b"2^24" in lib().dx_last_error()
+    # the limit is checked before an empty call returns, and only at head_dim 64 / 128: the head_dim 256
+    # kernel addresses with 64-bit pointers, so the same strides pass (empty calls, no launch)
+    def fp32_empty(d):
+        return status("dx_attn_prefill", P, P, P, P, P, P, 0, 64, 8, 4, d, 8 * d, 1 << 24, 1 << 24, 8 * d,
+                      f(0.0625), f(0.0), 0, 1, _lib.DX_F32, NUL, 0, NUL)
+
+    assert fp32_empty(128) == _lib.DX_ERR_UNSUPPORTED
+    assert fp32_empty(256) == _lib.DX_OK, lib().dx_last_error()
 
 
 def test_noalloc_attention_refuses_oversize_before_any_launch() -> None:

@@ -23,7 +23,8 @@ def test_attention_fixture_reproduces() -> None:
     # the fixture's inputs are bf16 values and its sequences never see each other
     q = from_bits(g["q_bits"])
     assert q.shape == (122, 4, 64) and np.isfinite(g["out_bf16"]).all()
-    assert np.abs(g["out_bf16"] - g["out_f32"]).max() < 2e-2
+    # bf16 and fp32 forms within the attention tolerance, 2e-2 of the output's largest magnitude
+    assert np.abs(g["out_bf16"] - g["out_f32"]).max() < 2e-2 * np.abs(g["out_f32"]).max()
 
 
 def test_forward_fixture_reproduces() -> None:

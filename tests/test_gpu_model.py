@@ -3,8 +3,10 @@
 Every forward is checked by tests/forward_parity.py: each layer against the oracle on the GPU's own
 input to that layer (bf16 output tolerance), the readout of the GPU's final hidden state within
 1e-3 absolute with the same argmax, and the free-running end-to-end distance from the exactly summed
-oracle measured beside the fp32 oracle's own drift (recorded; see that module for why bf16 rounding
-noise through depth puts it above 1e-3). The 9B and 27B shapes run at full depth, 42 and 46 layers.
+oracle within max(1e-3, 1.5 x the spread of fp32 oracles with other summation orders); see that
+module for why bf16 rounding noise through depth puts that drift above 1e-3 with random-init weights,
+and for the readout-temperature regime in which the 1e-3 bar itself is asserted at full depth. The 9B
+and 27B shapes run at full depth, 42 and 46 layers.
 """
 
 from __future__ import annotations
@@ -88,7 +90,9 @@ def test_full_depth_forward_matches_oracle(model: str, lengths: list[int]) -> No
     """The benchmark's shapes at full depth (9B: 42 layers, 27B: 46 layers) with the benchmark's
     random-init distributions, on two short requests whose ids and option labels come from the first
     4096 vocabulary rows: every layer against the oracle on the GPU's own input, the readout within
-    1e-3, and the end-to-end distance from the exactly summed oracle measured beside the fp32 oracle's."""
+    1e-3, the end-to-end distance from the exactly summed oracle within 1.5 x the fp32 floor, and the
+    same forward under the readout temperature 0.01, where the fp32 floor is below 3e-4, held to the
+    1e-3 bar with identical argmax wherever the truth's top-2 gap exceeds 2e-3."""
     from deciax_amd import gemma
 
     cfg = gemma.CONFIGS[model]
@@ -105,7 +109,7 @@ def test_full_depth_forward_matches_oracle(model: str, lengths: list[int]) -> No
             req.append([(int(p), int(r.integers(0, 4096))) for p in positions[used:used + k]])
             used += k
         options.append(req)
-    check_forward(f"{model} full depth {lengths}", w, gemma.pack_batch(ids, options))
+    check_forward(f"{model} full depth {lengths}", w, gemma.pack_batch(ids, options), readout_temperatures=(0.01,))
 
 
 def test_checkpoint_directory_forward_matches_oracle(tmp_path) -> None:

@@ -416,3 +416,23 @@ def test_flash_attention_rejects_bad_shapes() -> None:
         K.flash_attention(qkv, mask, heads=2, out_dtype=torch.float32)
     with pytest.raises(ValueError, match="qkv"):
         K.flash_attention(qkv[0], mask, heads=2)
+
+
+def test_offsets_registry_pairs_tensors_with_their_host_values() -> None:
+    """offsets_tensor remembers the host values a tensor was built from (so the readout validates
+    without a device read); other tensors, and tensors that are gone, are not known."""
+    import gc
+
+    import torch
+
+    from deciax_amd import kernels as K
+
+    t = K.offsets_tensor([0, 3, 5, 9], "cpu")
+    assert t.dtype == torch.int32 and t.tolist() == [0, 3, 5, 9]
+    assert K.known_offsets(t) == (0, 3, 5, 9)
+    assert K.known_offsets(t.clone()) is None
+    assert K.known_offsets(torch.tensor([0, 3, 5, 9], dtype=torch.int32)) is None
+    key = id(t)
+    del t
+    gc.collect()
+    assert key not in K._OFFSETS

@@ -209,3 +209,27 @@ def test_decode_kats() -> None:
     with pytest.raises(FloatingPointError, match="non-finite"):
         om.decode_probs(np.array([np.nan, 0.0], np.float32), [2])
     np.testing.assert_allclose(softmax(np.array([1000.0, 1000.0], np.float32)), [0.5, 0.5])
+
+
+@pytest.mark.parametrize("k", [1, 64, 100, 3584])
+def test_summation_orders_agree_with_the_exact_product(k: int) -> None:
+    """Every summation order of the oracle's matmul is the same product up to fp32 rounding (a dropped
+    or repeated K tile would be off by a whole tile's share), and in fp64 the orders coincide."""
+    from oracle.numerics import ORDERS, accumulation, matmul
+
+    r = np.random.Generator(np.random.PCG64(k))
+    a = r.normal(size=(7, k)).astype(np.float32)
+    b = r.normal(size=(k, 5)).astype(np.float32)
+    exact = a.astype(np.float64) @ b.astype(np.float64)
+    tol = 1e-6 * np.sqrt(k) * np.abs(a).max() * np.abs(b).max() * 8
+    got = {}
+    for order in ORDERS:
+        with accumulation(np.float32, order):
+            got[order] = matmul(a, b)
+        np.testing.assert_allclose(got[order], exact, rtol=0, atol=tol)
+        with accumulation(np.float64, order):  # summed in fp64, returned rounded once to fp32 (one ulp)
+            np.testing.assert_allclose(matmul(a, b), exact, rtol=2.0 ** -23, atol=1e-12)
+    if k > 64:  # the orders differ at the fp32 level, or they would not measure anything
+        assert any(not np.array_equal(got["blas"], got[o]) for o in ORDERS[1:])
+    if k > 128:  # with three tiles or more the walk direction changes the rounding too
+        assert not np.array_equal(got["k_tiles"], got["k_tiles_reversed"])
