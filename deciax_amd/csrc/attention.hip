@@ -145,6 +145,7 @@ attn_bf16_kernel(const uint16_t *__restrict__ Q, const uint16_t *__restrict__ K,
   constexpr int NDB = D / 32;
   constexpr int CPR = D / 8;            // 16-byte chunks per K row
   static_assert(WI >= 2 && WI % 2 == 0 && NI % BF_WAVES == 0, "tile too small for the wave count");
+  static_assert(BF_WAVES * 32 * D <= NSTAGE * STAGE, "the ring must hold every wave's 32 x D output tile");
   __shared__ __attribute__((aligned(1024))) uint16_t smem[NSTAGE * STAGE];
 
   // Grid order, the query tile index counted from the last (heaviest first):
@@ -419,22 +420,41 @@ attn_bf16_kernel(const uint16_t *__restrict__ Q, const uint16_t *__restrict__ K,
     }
     tile(kt, Flag<true>());
   }
+  // Every wave's ring loads have landed and no wave reads the ring any more: it now stages the output.
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
 
+  // Each lane holds 4-value pieces of its row qi scattered over the head's D columns; stored directly,
+  // every store instruction would touch 32 rows (32 cache lines, 8 bytes each). The wave writes its
+  // 32 x D bf16 tile to its own LDS region (row r's 16-byte chunk c at slot c ^ (r % CPR)), then each
+  // store instruction writes whole contiguous rows, 16 bytes per lane.
   lsum += __shfl_xor(lsum, 32, 64);
-  if (qi < len) {
-    float inv = 1.f / lsum;
-    if constexpr (KM) inv = lsum > 0.f ? inv : 0.f;
-    uint16_t *op = O + (start + qi) * o_stride + (long)h * D + lhalf * 4;
+  float inv = 1.f / lsum;
+  if constexpr (KM) inv = lsum > 0.f ? inv : 0.f;
+  // Lane indices derived anew here, through an opaque copy: values shared with the prologue would stay
+  // live across the key loop, and the loop's schedule then keeps fewer fragment reads in flight.
+  int el = (int)threadIdx.x & 63;
+  asm volatile("" : "+v"(el));
+  const int erow = el & 31, ehalf = el >> 5;
+  uint16_t *stage = smem + wave * 32 * D;
 #pragma unroll
-    for (int db = 0; db < NDB; ++db)
+  for (int db = 0; db < NDB; ++db)
 #pragma unroll
-      for (int grp = 0; grp < 4; ++grp) {
-        u32x2 w;
-        w[0] = pack_bf2(o[db][grp * 4 + 0] * inv, o[db][grp * 4 + 1] * inv);
-        w[1] = pack_bf2(o[db][grp * 4 + 2] * inv, o[db][grp * 4 + 3] * inv);
-        *reinterpret_cast<u32x2 *>(op + db * 32 + grp * 8) = w;
-      }
+    for (int grp = 0; grp < 4; ++grp) {
+      u32x2 w;
+      w[0] = pack_bf2(o[db][grp * 4 + 0] * inv, o[db][grp * 4 + 1] * inv);
+      w[1] = pack_bf2(o[db][grp * 4 + 2] * inv, o[db][grp * 4 + 3] * inv);
+      const int chunk = db * 4 + grp;  // 16-byte chunk of the row; this lane fills its half ehalf
+      *reinterpret_cast<u32x2 *>(stage + erow * D + ((chunk ^ (erow % CPR)) << 3) + ehalf * 4) = w;
+    }
+  __syncthreads();
+  constexpr int RPI = 64 / CPR;  // rows per store instruction
+#pragma unroll
+  for (int i = 0; i < 32 / RPI; ++i) {
+    const int r = i * RPI + el / CPR, c = el % CPR;
+    if (qw0 + r < len)
+      *reinterpret_cast<u32x4 *>(O + (start + qw0 + r) * o_stride + (long)h * D + c * 8) =
+          *reinterpret_cast<const u32x4 *>(stage + r * D + ((c ^ (r % CPR)) << 3));
   }
 }
 
