@@ -31,6 +31,7 @@ _i32p = POINTER(c_int32)
 # Argument types of every entry point, in header order.
 SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
     "dx_version": (c_char_p, []),
+    "dx_noalloc_init": (c_int, []),
     "dx_last_error": (c_char_p, []),
     "dx_device_arch": (c_int, [c_int, c_char_p, c_int]),
     "dx_attn_prefill": (

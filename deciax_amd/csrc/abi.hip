@@ -138,14 +138,25 @@ std::mutex g_scratch_mu;
 constexpr int MAX_DEVICES = 64;
 void *g_scratch[MAX_DEVICES] = {};
 
-// Device address of the current device's `scratch`, looked up on the first call on that device.
-int scratch_on_current_device(void **out) {
+// Device address of the current device's `scratch`, looked up once per device (by dx_noalloc_init or the
+// first allocation-free call). The lookup may load the library's code object on that device, which graph
+// capture does not allow: a call on a capturing `stream` that would need it is refused instead.
+int scratch_on_current_device(void **out, hipStream_t stream, bool from_init) {
   int dev = -1;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return fail(DX_ERR_RUNTIME, "hipGetDevice: %s", hipGetErrorString(e));
   SUPPORTED(dev >= 0 && dev < MAX_DEVICES, "attention: device %d beyond the %d the static scratch tracks", dev,
             MAX_DEVICES);
   std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch[dev] && !from_init) {
+    hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+    e = hipStreamIsCapturing(stream, &capture);
+    if (e != hipSuccess) return fail(DX_ERR_RUNTIME, "hipStreamIsCapturing: %s", hipGetErrorString(e));
+    SUPPORTED(capture == hipStreamCaptureStatusNone,
+              "attention_noalloc: device %d's static scratch is looked up outside graph capture; call "
+              "dx_noalloc_init() on this device before capturing",
+              dev);
+  }
   if (!g_scratch[dev]) {
     void *p = nullptr;
     e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
@@ -194,7 +205,7 @@ int attn_prefill(const void *q, const void *k, const void *v, const uint8_t *key
     SUPPORTED(need <= DX_NOALLOC_SCRATCH_BYTES,
               "attention_noalloc: V^T staging of %ld bytes exceeds the %ld-byte static scratch", (long)need,
               (long)DX_NOALLOC_SCRATCH_BYTES);
-    st = scratch_on_current_device(&workspace);
+    st = scratch_on_current_device(&workspace, as_stream(stream), false);
     if (st) return st;
     workspace_bytes = DX_NOALLOC_SCRATCH_BYTES;
   }
@@ -231,6 +242,11 @@ int dx_attn_prefill(const void *q, const void *k, const void *v, void *out, cons
   return attn_prefill(q, k, v, nullptr, out, seq_start, seq_len, num_seqs, max_seq_len, num_q_heads, num_kv_heads,
                       head_dim, q_row_stride, k_row_stride, v_row_stride, out_row_stride, scale, softcap, window,
                       causal, dtype, workspace, workspace_bytes, stream);
+}
+
+int dx_noalloc_init(void) {
+  void *p = nullptr;
+  return scratch_on_current_device(&p, nullptr, true);
 }
 
 int dx_attn_prefill_noalloc(const void *q, const void *k, const void *v, void *out, const int32_t *seq_start,

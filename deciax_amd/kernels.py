@@ -419,13 +419,23 @@ def attention_vt(q: torch.Tensor, k: torch.Tensor, vt: torch.Tensor, seq_start: 
     return out
 
 
+def noalloc_init() -> None:
+    """Look up the current device's static scratch of the allocation-free attention (outside graph
+    capture; idempotent)."""
+    call("dx_noalloc_init")
+
+
 def attention_varlen_noalloc(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, seq_start: torch.Tensor,
                              seq_len: torch.Tensor, max_seq_len: int, *, num_q_heads: int, num_kv_heads: int,
                              head_dim: int, scale: float, softcap: float = 0.0, window: int = 0, causal: bool = True,
                              out: torch.Tensor) -> torch.Tensor:
     """`attention_varlen` through dx_attn_prefill_noalloc: nothing is allocated (the caller passes
     `out`; the bf16 path stages V^T in the library's static per-GPU scratch of
-    DX_NOALLOC_SCRATCH_BYTES). Calls that overlap on one GPU race on that scratch."""
+    DX_NOALLOC_SCRATCH_BYTES). Calls that overlap on one GPU race on that scratch. Outside graph
+    capture the scratch's address is looked up first (dx_noalloc_init); a first call on a device made
+    under capture, without `noalloc_init()` beforehand, raises ValueError."""
+    if not torch.cuda.is_current_stream_capturing():
+        noalloc_init()
     dtype = q.dtype
     if dtype not in (BF16, F32):
         raise ValueError(f"attention: dtype must be bf16 or fp32, got {dtype}")

@@ -101,14 +101,24 @@ int64_t dx_attn_prefill_workspace(int32_t num_seqs, int32_t max_seq_len,
  * callers that cannot allocate device memory (code under HIP graph capture,
  * serving loops that forbid hipMalloc). The bf16 path stages V^T in a static
  * device array of DX_NOALLOC_SCRATCH_BYTES that the library holds on each GPU
- * it runs on until the process ends (its address is looked up on the first
- * call on a device); calls whose V^T staging, dx_attn_prefill_workspace(...)
- * bytes, exceeds it return DX_ERR_UNSUPPORTED. Nothing is allocated and
- * nothing needs clearing: the transpose writes every V^T column the attention
- * kernel reads. Every call on one GPU shares that GPU's array, so calls that
- * overlap on one GPU (concurrent streams or threads) race; serialise them.
- * Results are identical to dx_attn_prefill's. */
+ * it runs on until the process ends; calls whose V^T staging,
+ * dx_attn_prefill_workspace(...) bytes, exceeds it return DX_ERR_UNSUPPORTED.
+ * Nothing is allocated and nothing needs clearing: the transpose writes every
+ * V^T column the attention kernel reads. Every call on one GPU shares that
+ * GPU's array, so calls that overlap on one GPU (concurrent streams or
+ * threads) race; serialise them. Results are identical to dx_attn_prefill's.
+ * The array's device address is looked up once per device, by
+ * dx_noalloc_init or else by the first call on that device; that lookup is
+ * not allowed under graph capture, so a first call on a capturing stream
+ * returns DX_ERR_UNSUPPORTED: call dx_noalloc_init on each device before
+ * capturing. The address is kept for the life of the process; a device reset
+ * is not supported. */
 #define DX_NOALLOC_SCRATCH_BYTES (64LL << 20)
+
+/* Look up the current device's static scratch of dx_attn_prefill_noalloc
+ * (idempotent; call outside graph capture). No counterpart in the reference:
+ * for the callers that cannot allocate. Returns DX_OK or DX_ERR_RUNTIME. */
+int dx_noalloc_init(void);
 
 int dx_attn_prefill_noalloc(const void *q, const void *k, const void *v,
                             void *out, const int32_t *seq_start,
