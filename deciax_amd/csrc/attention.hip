@@ -381,9 +381,11 @@ attn_bf16_kernel(const uint16_t *__restrict__ Q, const uint16_t *__restrict__ K,
 #pragma unroll
     for (int kb = 0; kb < TK / 32; ++kb) block(sk, kt * TK + kb * 32, kb, masked);
     // tile kt + 1 has landed in every wave's share (the NSTAGE - 2 younger tiles may stay in flight)
-    // and every wave is done reading tile kt, whose stage the next iteration refills
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"((NSTAGE - 2) * WI) : "memory");
-    __syncthreads();
+    // and every wave is done reading tile kt, whose stage the next iteration refills. A plain s_barrier:
+    // __syncthreads would also wait for the younger tiles' loads (its fence waits for all LDS writes).
+    asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"((NSTAGE - 2) * WI) : "memory");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
   };
 
   // Tiles [ta, tb) hold no key this wave's rows cannot see (all blocks active, none masked): they run
@@ -411,8 +413,9 @@ attn_bf16_kernel(const uint16_t *__restrict__ Q, const uint16_t *__restrict__ K,
 
 #pragma unroll
   for (int i = 0; i < NSTAGE - 1; ++i) issue(min(kt0 + i, kt1 - 1), i);
-  asm volatile("s_waitcnt vmcnt(%0)" ::"n"((NSTAGE - 2) * WI) : "memory");
-  __syncthreads();
+  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"((NSTAGE - 2) * WI) : "memory");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_sched_barrier(0);
   for (int kt = kt0; kt < kt1; ++kt) {
     if (kt == ta) {
       for (; kt < tb; ++kt) tile(kt, Flag<false>());
