@@ -197,6 +197,8 @@ ATTN_CASES = [
     ([256, 219], 4, 4, 64, 64, 0.0, False),
     ([700], 4, 2, 256, 128, 0.0, True),
     ([64, 1, 2], 4, 1, 128, 0, 80.0, True),
+    ([0, 77, 33], 16, 4, 256, 0, 50.0, True),    # head_dim 256 at GQA 4, with an empty sequence
+    ([95, 160], 8, 8, 256, 32, 50.0, True),      # head_dim 256 without grouping, window 32
 ]
 
 
@@ -388,6 +390,7 @@ MASK_CASES = [
     (96, 130, 4, 1, 128, False, 0, 30.0, "bf16"),
     (77, 77, 4, 2, 64, True, 0, 20.0, "f32"),
     (64, 90, 8, 4, 128, False, 8, 0.0, "f32"),
+    (120, 120, 8, 2, 256, True, 0, 0.0, "bf16"),  # running-max softmax at head_dim 256, GQA 4
 ]
 
 
