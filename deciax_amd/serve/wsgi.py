@@ -257,6 +257,11 @@ def _read_body(environ: Mapping[str, Any]) -> tuple[bytes, Refusal | None]:
 
 
 class _Handler(WSGIRequestHandler):
+    # A client that declares a body and then stalls would otherwise hold its connection's thread for good
+    # (the admission counter only covers requests whose body has arrived): reads and writes on the socket
+    # time out after this many seconds and the connection is dropped.
+    timeout = 60
+
     def log_message(self, format: str, *args: Any) -> None:  # noqa: A002
         log.info("%s - %s", self.address_string(), format % args)
 

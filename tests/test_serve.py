@@ -7,6 +7,7 @@ from __future__ import annotations
 import http.client
 import json
 import threading
+import time
 from typing import Any
 
 import pytest
@@ -188,6 +189,40 @@ def test_http_round_trip() -> None:
         assert r.status == 200 and json.loads(r.read()) == {"status": "ok", "loaded": ["tiny"],
                                                             "default_model": "tiny", "device": "unknown"}
         conn.close()
+    finally:
+        server.shutdown()
+        server.server_close()
+
+
+def test_stalled_body_times_out(monkeypatch: pytest.MonkeyPatch) -> None:
+    """A client that declares a body and stops sending it loses its connection after the handler's
+    socket timeout, instead of holding the server thread; other clients are served meanwhile."""
+    import socket
+
+    from deciax_amd.serve import wsgi
+
+    monkeypatch.setattr(wsgi._Handler, "timeout", 0.5)
+    server = make_server(DecisionApp({"tiny": FakeDecider()}, "tiny"), "127.0.0.1", 0)
+    thread = threading.Thread(target=server.serve_forever, daemon=True)
+    thread.start()
+    try:
+        host, port = server.server_address[:2]
+        stalled = socket.create_connection((host, port), timeout=10)
+        stalled.sendall(b"POST /v1/systemone HTTP/1.1\r\nHost: x\r\nContent-Length: 100\r\n\r\n{\"questions\"")
+        conn = http.client.HTTPConnection(host, port, timeout=10)
+        conn.request("GET", "/health")
+        assert conn.getresponse().status == 200
+        conn.close()
+        started = time.monotonic()
+        received = b""
+        while True:  # the server answers the timed-out read with an error and closes the connection
+            chunk = stalled.recv(4096)
+            if not chunk:
+                break
+            received += chunk
+        assert time.monotonic() - started < 8
+        assert not received or received.startswith(b"HTTP/1.") and b" 200 " not in received.split(b"\r\n", 1)[0]
+        stalled.close()
     finally:
         server.shutdown()
         server.server_close()
