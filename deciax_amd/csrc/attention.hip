@@ -41,10 +41,15 @@
 namespace {
 
 constexpr int THREADS = 256;        // fp32 path and the V^T transpose
-constexpr int BF_WAVES = 8;         // bf16 path: two waves per SIMD
-constexpr int BF_THREADS = 64 * BF_WAVES;
 constexpr int BKV = 64;     // V^T block alignment of dx_transpose_v
-constexpr int NSTAGE = 4;   // LDS ring depth of the bf16 path
+// bf16 path: waves per workgroup and LDS ring depth. The long form, 8 waves (two per SIMD, 32 query rows
+// each) over a 4-stage ring (128 KB), runs one workgroup per CU. The short form, 4 waves over a 2-stage
+// ring (64 KB), runs two workgroups per CU that fall out of step with each other, so one's prologue,
+// epilogue and barrier waits overlap the other's key loop; it halves the query rows per staged K/V tile.
+// Head_dim 128 takes the short form when a query row sees 2048 keys or fewer on average (window <= 2048,
+// or causal sequences up to 4096): 27B heads, 8 x 2048 -4%, window 512 -12 to -15%, window 1024 -5 to
+// -10%, 16 x 3400 -2%; on longer spans it measured +0.2 to +1.1% (4 x 16384). Head_dim 256 keeps the long
+// form everywhere: the short one measured 6-11% slower on every shape but window 512 (within 1.5%).
 // bf16 grid order switch (see attn_bf16_kernel). Whole units per XCD measured 3-9% faster at 3257-4096
 // tokens (16 sequences, 9B and 27B heads), 2% slower at 8 x 3072 and 15% slower at 8 x 2048.
 constexpr int SHORT_SEQ = 3072;
@@ -112,9 +117,10 @@ DX_DEVICE int k_swz(int row) {
   else return (row >> 1) & 7;
 }
 
-// bf16 path: 8 waves (two per SIMD), wave w = 32 query rows of head g * G + w % G. Each 64-key tile is
-// processed in two 32-key halves (QK^T, softmax, PV per half) so a wave needs only 16 score registers and
-// the other wave on its SIMD can run MFMAs while this one is in the softmax.
+// bf16 path: WAVES waves (two per SIMD, the short or long form above), wave w = 32 query rows of head
+// g * G + w % G. Each 64-key tile is processed in two 32-key halves (QK^T, softmax, PV per half) so a wave
+// needs only 16 score registers and the other wave on its SIMD can run MFMAs while this one is in the
+// softmax.
 // Keys per tile: 32 at head_dim 256 (a 64-key tile would halve the ring depth), 64 below.
 template <int D>
 constexpr int tile_keys() { return D >= 256 ? 32 : 64; }
@@ -127,25 +133,25 @@ struct Flag {
 // KM: a per-key mask (key_bits, key_words 32-bit words per sequence; bit j of word w of sequence b is key
 // 32 w + j) hides keys beyond the causal / window rule. Every tile then takes the masked body, and a
 // query row that sees no key is written as zeros.
-template <int D, int G, int MODE, bool KM>
-__global__ void __launch_bounds__(BF_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2)))
+template <int D, int G, int MODE, bool KM, int WAVES, int NSTAGE>
+__global__ void __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2)))
 attn_bf16_kernel(const uint16_t *__restrict__ Q, const uint16_t *__restrict__ K, const uint16_t *__restrict__ Vt,
                  uint16_t *__restrict__ O, const int32_t *__restrict__ seq_start,
                  const int32_t *__restrict__ seq_len, const int32_t *__restrict__ vt_start, long vt_seq_stride,
                  int max_seq_len, long q_stride, long k_stride, long vt_ld, long o_stride, float scale,
                  float softcap, int window, int causal, const uint32_t *__restrict__ key_bits, int key_words) {
   constexpr int TK = tile_keys<D>();
-  constexpr int RG = BF_WAVES / G;      // 32-row groups per head
+  constexpr int RG = WAVES / G;         // 32-row groups per head
   constexpr int BQ = 32 * RG;           // query rows per workgroup
   constexpr int KST = TK * D;           // elements of the K tile [TK][D]; the V^T tile [D][TK] follows
   constexpr int STAGE = 2 * TK * D;
   constexpr int NI = TK * D / 256;      // direct-to-LDS instructions per tile (K then V^T), 1 KB each
-  constexpr int WI = NI / BF_WAVES;     // per wave
+  constexpr int WI = NI / WAVES;        // per wave
   constexpr int NKS = D / 16;
   constexpr int NDB = D / 32;
   constexpr int CPR = D / 8;            // 16-byte chunks per K row
-  static_assert(WI >= 2 && WI % 2 == 0 && NI % BF_WAVES == 0, "tile too small for the wave count");
-  static_assert(BF_WAVES * 32 * D <= NSTAGE * STAGE, "the ring must hold every wave's 32 x D output tile");
+  static_assert(WI >= 2 && WI % 2 == 0 && NI % WAVES == 0, "tile too small for the wave count");
+  static_assert(WAVES * 32 * D <= NSTAGE * STAGE, "the ring must hold every wave's 32 x D output tile");
   __shared__ __attribute__((aligned(1024))) uint16_t smem[NSTAGE * STAGE];
 
   // Grid order, the query tile index counted from the last (heaviest first):
@@ -819,20 +825,37 @@ vt_zero_tails_kernel(uint16_t *__restrict__ Vt, const int32_t *__restrict__ seq_
   if (row < vt_rows && j < ((len + 63) & ~63)) Vt[(long)row * vt_ld + vt_start[blockIdx.x] + j] = 0;
 }
 
-template <int D, int G>
-hipError_t launch_bf16_dg(const AttnArgs &a, hipStream_t s) {
-  constexpr int BQ = 32 * (BF_WAVES / G);
+template <int D, int G, int W, int NS>
+hipError_t launch_bf16_dgw(const AttnArgs &a, hipStream_t s) {
+  constexpr int BQ = 32 * (W / G);
   const unsigned ntiles = (a.max_seq_len + BQ - 1) / BQ;
   const dim3 grid = a.max_seq_len <= SHORT_SEQ ? dim3(a.hkv, a.num_seqs, ntiles) : dim3(ntiles, a.hkv, a.num_seqs);
   const bool fixed = a.softcap > 0.f && a.softcap <= 56.f;
-  auto kern = a.key_bits ? (fixed ? attn_bf16_kernel<D, G, MODE_FIXED, true> : attn_bf16_kernel<D, G, MODE_ONLINE, true>)
-                         : (fixed ? attn_bf16_kernel<D, G, MODE_FIXED, false> : attn_bf16_kernel<D, G, MODE_ONLINE, false>);
-  kern<<<grid, dim3(BF_THREADS), 0, s>>>(
+  auto kern = a.key_bits ? (fixed ? attn_bf16_kernel<D, G, MODE_FIXED, true, W, NS>
+                                  : attn_bf16_kernel<D, G, MODE_ONLINE, true, W, NS>)
+                         : (fixed ? attn_bf16_kernel<D, G, MODE_FIXED, false, W, NS>
+                                  : attn_bf16_kernel<D, G, MODE_ONLINE, false, W, NS>);
+  kern<<<grid, dim3(64 * W), 0, s>>>(
       static_cast<const uint16_t *>(a.q), static_cast<const uint16_t *>(a.k), static_cast<const uint16_t *>(a.v),
       static_cast<uint16_t *>(a.out), a.seq_start, a.seq_len, a.vt_start, a.vt_seq_stride, a.max_seq_len,
       a.q_stride, a.k_stride, a.v_stride, a.out_stride, a.scale, a.softcap, a.window, a.causal, a.key_bits,
       a.key_words);
   return hipGetLastError();
+}
+
+// Keys a query row sees on average: the window, or half the longest sequence when causal and unwindowed.
+inline long mean_key_span(const AttnArgs &a) {
+  const long n = a.max_seq_len;
+  const long w = a.window;
+  if (a.causal) return w > 0 ? (w < n ? w : n) : n / 2;
+  return w > 0 ? (2 * w < n ? 2 * w : n) : n;
+}
+
+template <int D, int G>
+hipError_t launch_bf16_dg(const AttnArgs &a, hipStream_t s) {
+  if constexpr (D == 128)
+    if (mean_key_span(a) <= 2048) return launch_bf16_dgw<D, G, 4, 2>(a, s);
+  return launch_bf16_dgw<D, G, 8, 4>(a, s);
 }
 
 template <int D>

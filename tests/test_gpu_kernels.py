@@ -248,6 +248,43 @@ def test_attention_vt_path_matches_generic() -> None:
         assert (vt_np[:, p0 + n:p0 + (n + 63) // 64 * 64] == 0).all()
 
 
+@pytest.mark.parametrize("hq,hkv", [(32, 16), (32, 8)])
+def test_attention_head_dim_128_short_and_long_forms_agree(hq: int, hkv: int) -> None:
+    """At head_dim 128 a launch whose query rows see 2048 keys or fewer on average runs two 4-wave
+    workgroups per CU, longer ones one 8-wave workgroup: the same rows in the same key order, so the
+    output is bit-identical. Declaring a longer max_seq_len (an upper bound of the lengths) flips the
+    form without changing any row; the short form is also checked against the oracle."""
+    import torch
+
+    from deciax_amd import kernels as K
+    from oracle.attention import attention_seq
+
+    lengths = [1000, 700, 1500, 33]
+    d = 128
+    say(f"attention head_dim 128 short vs long form hq={hq} hkv={hkv} lengths={lengths}")
+    q, k, v, starts = _packed_case(21 + hkv, lengths, hq, hkv, d)
+    rows = q.shape[0]
+    qd, kd, vd = (to_dev(a.reshape(rows, -1)) for a in (q, k, v))
+    padded = [(n + 63) // 64 * 64 for n in lengths]
+    vt_start = np.concatenate([[0], np.cumsum(padded)[:-1]])
+    vt = torch.zeros((hkv * d, int(sum(padded))), dtype=torch.bfloat16, device="cuda")
+    K.transpose_v(vd, vt, i32(starts), i32(lengths), i32(vt_start), max(lengths), num_kv_heads=hkv, head_dim=d)
+
+    def run(max_len: int) -> np.ndarray:
+        return to_np(K.attention_vt(qd, kd, vt, i32(starts), i32(lengths), i32(vt_start), max_len, num_q_heads=hq,
+                                    num_kv_heads=hkv, head_dim=d, scale=144 ** -0.5, softcap=50.0, window=0))
+
+    short = run(max(lengths))   # mean key span 750: the short form
+    np.testing.assert_array_equal(short, run(8192))  # span 4096: the long form
+    got = short.reshape(rows, hq, d)
+    r = rng(4)
+    for s, n in zip(starts, lengths):
+        qpos = np.unique(np.concatenate([[0, n - 1], r.choice(n, min(n, 6), replace=False)]))
+        want = attention_seq(q[s:s + n], k[s:s + n], v[s:s + n], scale=144 ** -0.5, softcap_value=50.0, window=0,
+                             query_pos=qpos, rounding="flash")
+        close(got[s + qpos], want, 2e-2, MEAN_REL["flash"])
+
+
 LONG_CASES = [
     # (hq, hkv, d, window, lengths): 24 or 48 (sequence, KV head) units, dealt out whole to the XCDs
     (16, 8, 256, 4096, [300, 5000, 4097]),
