@@ -141,6 +141,7 @@ readout_kernel(const uint16_t *__restrict__ hidden, const uint16_t *__restrict__
                long vocab, float eps, float softcap, float *__restrict__ logits, float *__restrict__ probs) {
   __shared__ float red[RO_WAVES];
   __shared__ float zs[RO_MAX_LDS];  // the question's logits, when it has at most RO_MAX_LDS options
+  __shared__ u32x4 wsh[MAXC * 64];  // the final norm's weights, 16-byte chunks
   const int q = blockIdx.x;
   // The offsets come from device memory: clamp the question's range into [0, num_options) so that a
   // malformed offset array can give wrong answers but never reads or writes outside the option arrays.
@@ -149,6 +150,11 @@ readout_kernel(const uint16_t *__restrict__ hidden, const uint16_t *__restrict__
   const bool in_lds = o1 - o0 <= RO_MAX_LDS;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int nch = d / 8;
+  // The norm weights, shared by every option, are staged in LDS once per workgroup while the offsets
+  // resolve: read from global memory inside the dot loop they cost one dependent round trip per 16-byte
+  // chunk, and held in registers beside both rows they spill at H 4608.
+  for (int c = threadIdx.x; c < nch; c += 64 * RO_WAVES) wsh[c] = *reinterpret_cast<const u32x4 *>(norm_w + c * 8);
+  __syncthreads();
   for (int o = o0 + wave; o < o1; o += RO_WAVES) {
     Row<MAXC> xr, er;
     const long prow = min(max((long)opt_pos[o], 0L), hidden_rows - 1);
@@ -161,7 +167,7 @@ readout_kernel(const uint16_t *__restrict__ hidden, const uint16_t *__restrict__
     for (int i = 0; i < MAXC; ++i) {
       const int c = lane + 64 * i;
       if (c < nch) {
-        const u32x4 wc = *reinterpret_cast<const u32x4 *>(norm_w + c * 8);  // shared by every option: an L2 hit
+        const u32x4 wc = wsh[c];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const uint32_t g = pack_bf2((lo_bf(xr.c[i][j]) * inv) * (1.f + lo_bf(wc[j])),
