@@ -133,11 +133,11 @@ template <int MAXC, bool POST, bool NEXT, bool COHERENT>
 DX_DEVICE void add_rmsnorm_row(const uint16_t *y, const uint16_t *post_w, uint16_t *x, const uint16_t *next_w,
                                uint16_t *h, int d, float eps, int lane) {
   const int nch = d / 8;
-  // Rows of up to 8 chunks per lane (H <= 4096) request the norm weights with the rows (the next
-  // norm's once the first is used), so their latency hides behind the row loads and the sums
-  // (H 3584: -3.8%). Longer rows read them where used: a third register row costs them occupancy
-  // (H 4608: +14%).
-  constexpr bool PREFETCH = MAXC <= 8;
+  // Rows of up to 12 chunks per lane request the norm weights with the rows (the next norm's once the
+  // first is used), so their latency hides behind the row loads and the sums (H 3584: -3.8%; H 4608 in
+  // 12-chunk rows: -12.9%). 16-chunk rows read them where used: a third 64-register row costs them
+  // occupancy (H 4608 in 16-chunk rows: +14%).
+  constexpr bool PREFETCH = MAXC <= 12;
   Row<MAXC> yr, xr, wr;
   if constexpr (COHERENT) load_row_coherent(yr, y, nch, lane);
   else load_row(yr, y, nch, lane);
