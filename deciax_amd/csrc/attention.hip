@@ -564,9 +564,9 @@ attn_f32_kernel(const float *__restrict__ Q, const float *__restrict__ K, const 
 //   32-63). Lane l then holds query l % 32 and keys (r / 4) 8 + (l / 32) 4 + r % 4 of the block.
 //   O^T += V^T P^T: MFMA step i contracts the two keys the lane halves hold in register i, so each lane
 //   feeds its own probabilities as the B operand and reads V[key][d] for its half's key.
-// The next block's K and V come from global memory into registers during this block's QK^T and
-// softmax / PV respectively, and go to LDS once the region's previous reads are done (LDS operations of
-// one wave complete in order).
+// The next block's K and V are requested from global memory into registers at the start of this block
+// and go to LDS once the region's previous reads are done (K after this block's PV, V at the start of the
+// next block; LDS operations of one wave complete in order), so each load has a whole block to land.
 constexpr int F_WAVES = 4;
 
 DX_DEVICE floatx16 mfma32_f32(float a, float b, floatx16 c) {
@@ -636,7 +636,9 @@ attn_f32_mfma_kernel(const float *__restrict__ Q, const float *__restrict__ K, c
   const float *const vseq = V + start * v_stride + (long)g * D;
   float4 kr[LPL], vr[LPL];
   auto rsrc = [&](const float *base, long stride, int kb) {
-    const long rows = min(max(len - kb * 32, 0), 32);  // the block's rows only: 32-bit byte counts
+    // the block's rows only (32-bit byte counts); wave-uniform, which the compiler is told so that the
+    // descriptor stays in scalar registers (a vector one costs a waterfall loop around every load)
+    const long rows = __builtin_amdgcn_readfirstlane(min(max(len - kb * 32, 0), 32));
     return __builtin_amdgcn_make_buffer_rsrc((void *)(base + (long)kb * 32 * stride), (short)0,
                                              (int)(rows * stride * 4), 0x00020000);
   };
@@ -679,40 +681,57 @@ attn_f32_mfma_kernel(const float *__restrict__ Q, const float *__restrict__ K, c
     put_v();
     const int nb = kb + F_WAVES;
     const bool more = nb < kb1;
-    if (more) fetch_k(nb);
+    if (more) {  // the next block's K and V load during this whole block
+      fetch_k(nb);
+      fetch_v(nb);
+    }
     floatx16 s;
 #pragma unroll
     for (int r = 0; r < 16; ++r) s[r] = 0.f;
     {
+      // every K fragment of the block is requested before the first MFMA: one LDS round trip per block
+      // instead of one per four MFMAs of the dependent chain
       const float *kp = ks + lrow * KP + hh * DH;
+      float4 kv[DH / 4];
 #pragma unroll
-      for (int j = 0; j < DH; j += 4) {
-        const float4 kv = *reinterpret_cast<const float4 *>(kp + j);
-        s = mfma32_f32(kv.x, qf[j], s);
-        s = mfma32_f32(kv.y, qf[j + 1], s);
-        s = mfma32_f32(kv.z, qf[j + 2], s);
-        s = mfma32_f32(kv.w, qf[j + 3], s);
+      for (int j = 0; j < DH / 4; ++j) kv[j] = *reinterpret_cast<const float4 *>(kp + 4 * j);
+      __builtin_amdgcn_sched_barrier(0);  // the scheduler would otherwise sink each read to its MFMAs
+#pragma unroll
+      for (int j = 0; j < DH / 4; ++j) {
+        s = mfma32_f32(kv[j].x, qf[4 * j], s);
+        s = mfma32_f32(kv[j].y, qf[4 * j + 1], s);
+        s = mfma32_f32(kv[j].z, qf[4 * j + 2], s);
+        s = mfma32_f32(kv[j].w, qf[4 * j + 3], s);
       }
     }
-    if (more) {
-      put_k();
-      fetch_v(nb);
-    }
-    // score r is key kb 32 + (r / 4) 8 + 4 hh + r % 4 of query qi
+    // score r is key kb 32 + (r / 4) 8 + 4 hh + r % 4 of query qi. The softcap and key-mask tests are
+    // taken once per block, outside the per-score loops.
     const int kbase = kb * 32 + 4 * hh;
+    if (softcap > 0.f) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        float x = s[r] * scale;
+        x = softcap - 2.f * softcap * fast_rcp(1.f + fast_exp2(x * cap2));  // cap tanh(x / cap)
+        s[r] = x * LOG2E;
+      }
+    } else {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float x = s[r] * scale;
+        s[r] = x * LOG2E;
+      }
+    }
     uint32_t vis = 0;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) vis |= (uint32_t)visible(qi, kbase + (r >> 2) * 8 + (r & 3), len, window, causal) << r;
+    if (key_mask) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r)  // read only for visible keys, which lie inside the sequence
+        if (((vis >> r) & 1u) && !key_mask[start + kbase + (r >> 2) * 8 + (r & 3)]) vis &= ~(1u << r);
+    }
     float tmax = NEG_BIG;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int key = kbase + (r >> 2) * 8 + (r & 3);
-      float x = s[r] * scale;
-      if (softcap > 0.f) x = softcap - 2.f * softcap * fast_rcp(1.f + fast_exp2(x * cap2));  // cap tanh(x / cap)
-      x *= LOG2E;
-      const bool v = visible(qi, key, len, window, causal) && (!key_mask || key_mask[start + key]);
-      vis |= (uint32_t)v << r;
-      s[r] = x;
-      if (v) tmax = fmaxf(tmax, x);
-    }
+    for (int r = 0; r < 16; ++r) tmax = ((vis >> r) & 1u) ? fmaxf(tmax, s[r]) : tmax;
     tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
     const float mnew = fmaxf(m, tmax);
     const float alpha = fast_exp2(m - mnew);
@@ -735,6 +754,7 @@ attn_f32_mfma_kernel(const float *__restrict__ Q, const float *__restrict__ K, c
 #pragma unroll
       for (int i = 0; i < 16; ++i)
         o[db] = mfma32_f32(vs[((i >> 2) * 8 + 4 * hh + (i & 3)) * VP + db * 32 + lrow], s[i], o[db]);
+    if (more) put_k();
   }
 
   // merge the waves' states: wave w writes O^T, m and the row sum into its region, then every thread
