@@ -111,7 +111,9 @@ DX_DEVICE __amdgpu_buffer_rsrc_t make_rsrc(const uint16_t *base, long bytes) {
 template <int BM>
 DX_DEVICE void norm_epilogue(const uint16_t *Y, int M, int N, long ldy, int m0, int tm, int num_n,
                              const NormEpilogue &ne, int *flag) {
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // wave is wave-uniform, which the compiler is told: each row's coherent-load descriptor then stays in
+  // scalar registers instead of costing a waterfall loop around every load
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this thread's y stores have reached memory
   __syncthreads();  // ... every thread's; the staged tile in LDS is no longer read, so `flag` may reuse it
   if (tid == 0)
