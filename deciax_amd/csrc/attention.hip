@@ -131,8 +131,8 @@ struct Flag {
 };
 
 // KM: a per-key mask (key_bits, key_words 32-bit words per sequence; bit j of word w of sequence b is key
-// 32 w + j) hides keys beyond the causal / window rule. Every tile then takes the masked body, and a
-// query row that sees no key is written as zeros.
+// 32 w + j) hides keys beyond the causal / window rule. Tiles that hold a masked key take the masked body,
+// and a query row that sees no key is written as zeros.
 template <int D, int G, int MODE, bool KM, int WAVES, int NSTAGE>
 __global__ void __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2)))
 attn_bf16_kernel(const uint16_t *__restrict__ Q, const uint16_t *__restrict__ K, const uint16_t *__restrict__ Vt,
@@ -398,7 +398,7 @@ attn_bf16_kernel(const uint16_t *__restrict__ Q, const uint16_t *__restrict__ K,
   // without any mask code. The tiles before and after take the masked body. Every wave runs one
   // iteration (one barrier) per tile, whichever body.
   int ta = kt1, tb = kt1;
-  if (!KM && qw1 < len) {
+  if (qw1 < len) {
     int lo_u = 0, hi_u = len - 32;  // first / last kbase of an unmasked block
     if (causal) {
       hi_u = min(hi_u, qw0 - 31);
@@ -422,12 +422,35 @@ attn_bf16_kernel(const uint16_t *__restrict__ Q, const uint16_t *__restrict__ K,
   asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"((NSTAGE - 2) * WI) : "memory");
   __builtin_amdgcn_s_barrier();
   __builtin_amdgcn_sched_barrier(0);
-  for (int kt = kt0; kt < kt1; ++kt) {
-    if (kt == ta) {
-      for (; kt < tb; ++kt) tile(kt, Flag<false>());
-      if (kt == kt1) break;
+  if constexpr (KM) {
+    // A tile of [ta, tb) whose keys the mask keeps entirely takes the unmasked body as well. Its mask
+    // words are requested one tile ahead (scalar loads, which the tile's barrier wait covers).
+    const uint32_t *const kw = key_bits + (long)b * key_words;
+    auto full = [&](int kt) {
+      bool f = true;
+#pragma unroll
+      for (int i = 0; i < TK / 32; ++i) f = f && kw[kt * (TK / 32) + i] == 0xffffffffu;
+      return f;
+    };
+    for (int kt = kt0; kt < kt1; ++kt) {
+      if (kt >= ta && kt < tb && full(kt)) {
+        // a run of interior tiles whose keys the mask keeps, each next tile's words read before this one
+        for (bool more = true; more; ++kt) {
+          more = kt + 1 < tb && full(kt + 1);
+          tile(kt, Flag<false>());
+        }
+        if (kt == kt1) break;
+      }
+      tile(kt, Flag<true>());
     }
-    tile(kt, Flag<true>());
+  } else {
+    for (int kt = kt0; kt < kt1; ++kt) {
+      if (kt == ta) {
+        for (; kt < tb; ++kt) tile(kt, Flag<false>());
+        if (kt == kt1) break;
+      }
+      tile(kt, Flag<true>());
+    }
   }
   // Every wave's ring loads have landed and no wave reads the ring any more: it now stages the output.
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");

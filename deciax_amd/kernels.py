@@ -535,13 +535,17 @@ def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, key_mask: torch
     length = max(nq, nk)
     if nk == 0:
         raise ValueError("attention: need at least one key")
-    # One sequence per batch row of `length` rows: queries padded past Q (dropped afterwards), keys
-    # padded past K (masked out).
-    qp = torch.zeros((b, length, hq, d), dtype=q.dtype, device=q.device)
-    kp = torch.zeros((b, length, hkv, d), dtype=q.dtype, device=q.device)
-    vp = torch.zeros_like(kp)
-    mp = torch.zeros((b, length), dtype=torch.bool, device=q.device)
-    qp[:, :nq], kp[:, :nk], vp[:, :nk], mp[:, :nk] = q, k, v, mask
+    if nq == nk and q.is_contiguous() and k.is_contiguous() and v.is_contiguous():
+        # already one sequence of `length` rows per batch row: the kernels read the tensors in place
+        qp, kp, vp, mp = q, k, v, mask
+    else:
+        # One sequence per batch row of `length` rows: queries padded past Q (dropped afterwards), keys
+        # padded past K (masked out).
+        qp = torch.zeros((b, length, hq, d), dtype=q.dtype, device=q.device)
+        kp = torch.zeros((b, length, hkv, d), dtype=q.dtype, device=q.device)
+        vp = torch.zeros_like(kp)
+        mp = torch.zeros((b, length), dtype=torch.bool, device=q.device)
+        qp[:, :nq], kp[:, :nk], vp[:, :nk], mp[:, :nk] = q, k, v, mask
     starts = torch.arange(b, device=q.device, dtype=torch.int32) * length
     lengths = torch.full((b,), length, device=q.device, dtype=torch.int32)
     rows = b * length

@@ -431,6 +431,37 @@ MASK_CASES = [
 ]
 
 
+@pytest.mark.parametrize("hq,hkv,d,window", [(16, 8, 256, 0), (32, 16, 128, 300), (8, 4, 64, 0)])
+def test_attention_kept_mask_tiles_take_the_unmasked_body(hq: int, hkv: int, d: int, window: int) -> None:
+    """Key-mask launches give interior tiles whose mask words keep every key the unmasked body: with an
+    all-ones mask the output is bit-identical to the unmasked kernel's, and a mask with holes in some
+    tiles still matches the oracle (the holes' tiles take the masked body)."""
+    import torch
+
+    from deciax_amd import kernels as K
+    from oracle.attention import attention_seq
+
+    lengths = [700, 1300, 64]
+    say(f"attention kept-mask tiles hq={hq} hkv={hkv} d={d} window={window} lengths={lengths}")
+    q, k, v, starts = _packed_case(31 + d, lengths, hq, hkv, d)
+    rows = q.shape[0]
+    qd, kd, vd = (to_dev(a.reshape(rows, -1)) for a in (q, k, v))
+    kw = dict(num_q_heads=hq, num_kv_heads=hkv, head_dim=d, scale=d ** -0.5, softcap=50.0, window=window)
+    ones = torch.ones(rows, dtype=torch.uint8, device="cuda")
+    plain = K.attention_varlen(qd, kd, vd, i32(starts), i32(lengths), max(lengths), **kw)
+    kept = K.attention_masked(qd, kd, vd, ones, i32(starts), i32(lengths), max(lengths), **kw)
+    np.testing.assert_array_equal(to_np(kept), to_np(plain))
+    holes = np.ones(rows, dtype=bool)
+    holes[starts[1] + np.array([5, 6, 400, 999])] = False  # three tiles of the second sequence
+    got = to_np(K.attention_masked(qd, kd, vd, torch.from_numpy(holes.astype(np.uint8)).cuda(), i32(starts), i32(lengths),
+                                   max(lengths), **kw)).reshape(rows, hq, d)
+    s, n = int(starts[1]), lengths[1]
+    qpos = np.array([0, 7, 401, 650, 1000, n - 1])
+    want = attention_seq(q[s:s + n], k[s:s + n], v[s:s + n], scale=d ** -0.5, softcap_value=50.0, window=window,
+                         query_pos=qpos, rounding="flash", key_mask=holes[s:s + n])
+    close(got[s + qpos], want, 2e-2, MEAN_REL["flash"])
+
+
 @pytest.mark.parametrize("nq,nk,hq,hkv,d,causal,window,softcap,dtype", MASK_CASES)
 def test_attention_arbitrary_key_mask(nq, nk, hq, hkv, d, causal, window, softcap, dtype) -> None:
     """blocked.attention's interface in full (src/deciax/kernels/attention/blocked.py:9-32): [B, Q] queries
