@@ -552,10 +552,10 @@ def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, key_mask: torch
     flat = dict(num_q_heads=hq, num_kv_heads=hkv, head_dim=d, scale=scale, softcap=softcap, window=window,
                 causal=causal)
     args = (qp.reshape(rows, hq * d), kp.reshape(rows, hkv * d), vp.reshape(rows, hkv * d))
-    if bool(mp.all()):
-        out = attention_varlen(*args, starts, lengths, length, **flat)
-    else:
-        out = attention_masked(*args, mp.reshape(rows), starts, lengths, length, **flat)
+    # Always the key-mask kernel: tiles whose keys the mask keeps run its unmasked body, so a full mask
+    # costs about what the maskless kernel does, bit for bit the same output, and asking whether the mask
+    # is full would stall the stream for a host round trip.
+    out = attention_masked(*args, mp.reshape(rows), starts, lengths, length, **flat)
     out = out.reshape(b, length, hq, d)[:, :nq]
     empty = _visible_counts(mask, nq, causal, window) == 0
     if bool(empty.any()):
