@@ -535,9 +535,20 @@ def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, key_mask: torch
     length = max(nq, nk)
     if nk == 0:
         raise ValueError("attention: need at least one key")
-    if nq == nk and q.is_contiguous() and k.is_contiguous() and v.is_contiguous():
+
+    def rows_view(t: torch.Tensor, h: int) -> torch.Tensor | None:
+        # [B, L, h, D] as [B L, h D] rows without a copy (row-strided views, such as slices of a packed
+        # q | k | v, included); None when the strides do not allow it
+        try:
+            return t.view(b * length, h * d)
+        except RuntimeError:
+            return None
+
+    flat = [rows_view(q, hq), rows_view(k, hkv), rows_view(v, hkv)] if nq == nk else [None]
+    if all(x is not None for x in flat):
         # already one sequence of `length` rows per batch row: the kernels read the tensors in place
-        qp, kp, vp, mp = q, k, v, mask
+        qp, kp, vp = flat
+        mp = mask
     else:
         # One sequence per batch row of `length` rows: queries padded past Q (dropped afterwards), keys
         # padded past K (masked out).
@@ -549,13 +560,13 @@ def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, key_mask: torch
     starts = torch.arange(b, device=q.device, dtype=torch.int32) * length
     lengths = torch.full((b,), length, device=q.device, dtype=torch.int32)
     rows = b * length
-    flat = dict(num_q_heads=hq, num_kv_heads=hkv, head_dim=d, scale=scale, softcap=softcap, window=window,
-                causal=causal)
+    kw = dict(num_q_heads=hq, num_kv_heads=hkv, head_dim=d, scale=scale, softcap=softcap, window=window,
+              causal=causal)
     args = (qp.reshape(rows, hq * d), kp.reshape(rows, hkv * d), vp.reshape(rows, hkv * d))
     # Always the key-mask kernel: tiles whose keys the mask keeps run its unmasked body, so a full mask
     # costs about what the maskless kernel does, bit for bit the same output, and asking whether the mask
     # is full would stall the stream for a host round trip.
-    out = attention_masked(*args, mp.reshape(rows), starts, lengths, length, **flat)
+    out = attention_masked(*args, mp.reshape(rows), starts, lengths, length, **kw)
     out = out.reshape(b, length, hq, d)[:, :nq]
     empty = _visible_counts(mask, nq, causal, window) == 0
     if bool(empty.any()):
